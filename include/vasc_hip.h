@@ -1,0 +1,200 @@
+/*
+ * vasc_hip.h -- C-ABI of the MI355X (gfx950) sparse global-attention path.
+ *
+ * Plain pointers, 64-bit sizes and element strides, an explicit HIP stream
+ * (passed as void*, NULL = the legacy default stream) and an int status.
+ * No entry point allocates device memory: scratch comes from a caller
+ * buffer sized by the matching *_workspace_size query. Entry points are
+ * safe to call from any host thread on distinct streams; the only mutable
+ * global is the thread-local error string returned by vasc_last_error().
+ *
+ * Tensors are bfloat16 (passed as uint16_t bit patterns) unless noted.
+ * "[B,H,T,D] strided" means element (b,h,t,d) lives at
+ *   ptr[b*stride_b + h*stride_h + t*stride_t + d]   (d is contiguous).
+ *
+ * Reference interfaces replaced (paths relative to /root/reference; ZIP: is
+ * a member of third_party/spargeattn.zip under spargeattn/):
+ *   predict_attention ........ src/sparse_vggt/models/attention.py:31-104
+ *   _mean_pool_contiguous_value_blocks ... src/sparse_vggt/utils/sparse_wrapper.py:2839-2861
+ *   get_block_mask ........... sparse_wrapper.py:1199-1268
+ *   get_cosa_value_risk_pair_debt_mask ... sparse_wrapper.py:3632-4098
+ *   block_map_lut_triton ..... ZIP:spas_sage_attn/utils.py:54-87
+ *   _qattn.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf[_with_pv_threshold]
+ *                              ZIP:csrc/qattn/attn_cuda.h:19-45, pybind.cpp:5-13
+ */
+#ifndef VASC_HIP_H
+#define VASC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VASC_OK 0
+#define VASC_ERR_ARGUMENT 1    /* invalid pointer, size or stride          */
+#define VASC_ERR_UNSUPPORTED 2 /* valid request outside the built variants */
+#define VASC_ERR_HIP 3         /* a HIP runtime call failed                */
+
+#define VASC_MODE_TOPK 0
+#define VASC_MODE_VASC 1
+
+/* Message of the last non-zero status returned on the calling thread. */
+const char *vasc_last_error(void);
+
+/* ABI revision of this header (bumped on any signature change). */
+int vasc_abi_version(void);
+
+/*
+ * Kernel 1a: block mean pooling (avg_pool1d ceil_mode semantics: the tail
+ * block averages its real tokens) of Q over block_q tokens and of K and V
+ * over block_k tokens, each mean rounded to bfloat16 as the reference does
+ * under bf16 autocast, plus the pair innovation of the pooled V
+ * (0.5*sqrt(mean_d (V[2p]-V[2p+1])^2), sparse_wrapper.py:3733-3740).
+ * Replaces the pooling of predict_attention (attention.py:60-68) and
+ * _mean_pool_contiguous_value_blocks (sparse_wrapper.py:2839-2861).
+ * Any of q/k/v may be NULL to skip it (innovation needs v).
+ * Outputs are contiguous: pooled_q [B,H,ceil(nq/block_q),d],
+ * pooled_k / pooled_v [B,H,ceil(nk/block_k),d], innovation
+ * [B,H,ceil(ceil(nk/block_k)/2)] float32.
+ * Built variant: d == 64, block_q == 128, block_k == 64.
+ */
+int vasc_pool_qkv(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                  const uint16_t *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                  const uint16_t *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                  int64_t B, int64_t H, int64_t nq, int64_t nk, int64_t d,
+                  int64_t block_q, int64_t block_k,
+                  uint16_t *pooled_q, uint16_t *pooled_k, uint16_t *pooled_v,
+                  float *innovation, void *stream);
+
+/*
+ * Kernel 1b: pooled attention probabilities
+ *   prob = softmax_k( bf16( bf16(pooled_q . pooled_k) * scale ) )  (fp32)
+ * i.e. the score/softmax of predict_attention (attention.py:97-101) with the
+ * roundings of its bf16 autocast matmul. round_bf16 = 0 skips both
+ * bfloat16 roundings. pooled_q [B,H,qb,d], pooled_k [B,H,kb,d] contiguous;
+ * prob [B,H,qb,kb] float32 contiguous. Built variant: d == 64.
+ */
+int vasc_pooled_softmax(const uint16_t *pooled_q, const uint16_t *pooled_k,
+                        int64_t B, int64_t H, int64_t qb, int64_t kb, int64_t d,
+                        float scale, int32_t round_bf16, float *prob,
+                        void *stream);
+
+/*
+ * Pair innovation of given float32 pooled values [B,H,kb,d] (contiguous),
+ * bit-identical to the innovation written by vasc_pool_qkv for the same
+ * pooled values (sparse_wrapper.py:3733-3740). NaN -> 0, +-inf -> +-FLT_MAX
+ * first (sparse_wrapper.py:3690-3694). Built variant: d == 64.
+ */
+int vasc_pair_innovation(const float *pooled_v, int64_t B, int64_t H,
+                         int64_t kb, int64_t d, float *innovation,
+                         void *stream);
+
+/* Bytes of workspace vasc_select_blocks needs for these sizes. */
+size_t vasc_select_workspace_size(int64_t B, int64_t H, int64_t q_blocks,
+                                  int64_t k_blocks);
+
+/*
+ * Kernel 2: per-row block selection writing ascending index lists.
+ *
+ * mode VASC_MODE_TOPK: get_block_mask top-k (sparse_wrapper.py:1199-1268)
+ *   keeping the max(topk,1) largest scores per row, ties to the lower index.
+ * mode VASC_MODE_VASC: get_cosa_value_risk_pair_debt_mask
+ *   (sparse_wrapper.py:3632-4098) in the release configuration, including
+ *   the ledger settlement of the previous layer, the global service gate,
+ *   conservative arrival/debt projection, and the QK-admission service for
+ *   the next layer.
+ *
+ * score       [B,H,Q,K] float32 contiguous pooled probabilities.
+ * innovation  [B,H,ceil(K/2)] float32 (VASC only).
+ * topk        base budget int(K*(1-s)); the fill rule raises 0 to 1.
+ * row_cap     optional [B,H,Q] int32 per-row QK budget (VASC); NULL derives
+ *             it from topk and force_last as block_sparse_attn_cuda does.
+ * protected_mask optional [B,H,Q,K] uint8 (VASC): priority FLT_MAX.
+ * force_last  mixed tail block K-1: kept in TOPK, protected in VASC and
+ *             counted in the derived capacity (sparse_wrapper.py:7599-7662).
+ * max_capacity M (VASC): at most M blocks per row (the capacity hint).
+ * sink_blocks trailing always-on blocks K..K+sink-1 appended to each list.
+ * debt_in, pending_arrival, prev_service [B,H,P] float32, each may be NULL
+ *             (NULL pending = no previous layer to settle).
+ * debt_out, arrival_out, service_out [B,H,P] float32 (VASC, required).
+ * gate_out    optional int32 scalar: 1 when the debt priority was used.
+ * priority_out optional [B,H,Q,K] float32 execution priority.
+ * mask_out    optional [B,H,Q,K] uint8 support of the patch blocks.
+ * index_out   [B,H,Q,width] int32 ascending block indices (count entries
+ *             valid, rest untouched); count_out [B,H,Q] int32.
+ * Built variant: K <= 8192.
+ */
+int vasc_select_blocks(const float *score, const float *innovation,
+                       int64_t B, int64_t H, int64_t Q, int64_t K,
+                       int32_t mode, int32_t topk, const int32_t *row_cap,
+                       const uint8_t *protected_mask, int32_t force_last,
+                       int32_t max_capacity, int32_t sink_blocks,
+                       const float *debt_in, const float *pending_arrival,
+                       const float *prev_service, float *debt_out,
+                       float *arrival_out, float *service_out,
+                       int32_t *gate_out, float *priority_out,
+                       uint8_t *mask_out, int32_t *index_out, int64_t width,
+                       int32_t *count_out, void *workspace,
+                       size_t workspace_bytes, void *stream);
+
+/*
+ * Terminal ledger settlement (finalize_cosa_value_risk_pair_debt,
+ * sparse_wrapper.py:4101-4177): debt_out = max(debt_in + pending - service, 0)
+ * elementwise over n floats; debt_in may be NULL (zeros).
+ */
+int vasc_settle_terminal(const float *debt_in, const float *pending_arrival,
+                         const float *service, int64_t n, float *debt_out,
+                         void *stream);
+
+/* Elements (bf16) of the packed V buffer for these sizes. */
+int64_t vasc_packed_v_elems(int64_t B, int64_t H, int64_t nk, int64_t d);
+
+/*
+ * Kernel 3: pack V [B,H,nk,d] (strided) into per-64-key-block transposed
+ * tiles vt [B,H,ceil(nk/64),d,64] (contiguous), keys permuted into the
+ * MFMA operand order of the attention kernel and zero padded past nk.
+ * Precedent: SpargeAttn's TransposePadPermuteKernel (ZIP:csrc/fused/fused.cu:26-78).
+ * Built variant: d == 64.
+ */
+int vasc_pack_v(const uint16_t *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                int64_t B, int64_t H, int64_t nk, int64_t d, uint16_t *vt,
+                void *stream);
+
+/*
+ * Kernel 4: block-sparse flash attention forward, bf16 QK^T and PV on MFMA,
+ * fp32 online softmax. Query block i (128 rows) attends to the 64-key blocks
+ * listed in block_index[b,h,i,0:block_count[b,h,i]]; keys >= nk are masked.
+ * index_is_delta = 0: absolute ascending indices (vasc_select_blocks);
+ * index_is_delta = 1: SpargeAttn's delta LUT (first entry absolute).
+ * Out-of-range blocks are skipped; rows with count 0 are written as zeros.
+ * Replaces _qattn.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf
+ * (ZIP:csrc/qattn/attn_cuda.h:19-32) with bf16 inputs instead of int8 +
+ * scales. q, o [B,H,nq,d] strided; k [B,H,nk,d] strided; vt from
+ * vasc_pack_v. Built variant: d == 64.
+ */
+int vasc_block_sparse_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
+                               int64_t q_st, const uint16_t *k, int64_t k_sb,
+                               int64_t k_sh, int64_t k_st, const uint16_t *vt,
+                               uint16_t *o, int64_t o_sb, int64_t o_sh,
+                               int64_t o_st, int64_t B, int64_t H, int64_t nq,
+                               int64_t nk, int64_t d,
+                               const int32_t *block_index, int64_t index_width,
+                               const int32_t *block_count,
+                               int32_t index_is_delta, float sm_scale,
+                               void *stream);
+
+/* Dense variant of kernel 4: every query block attends to all key blocks. */
+int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
+                        int64_t q_st, const uint16_t *k, int64_t k_sb,
+                        int64_t k_sh, int64_t k_st, const uint16_t *vt,
+                        uint16_t *o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                        int64_t B, int64_t H, int64_t nq, int64_t nk,
+                        int64_t d, float sm_scale, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VASC_HIP_H */

@@ -1,0 +1,63 @@
+"""CPU restatement of block-sparse softmax attention.
+
+TEST INFRASTRUCTURE (see ``oracle/__init__.py``).
+
+Semantics of SpargeAttn's block-sparse kernel
+(``csrc/qattn/qk_int_sv_f16_cuda_sm80.cuh:42-738`` inside
+``third_party/spargeattn.zip``): query block ``i`` (``block_q`` rows) attends
+to the union of its listed ``block_k``-key blocks; keys at or beyond the
+sequence end are excluded (the kernel masks them to -5e6 on the final block,
+``.cuh:585``); softmax is exact (base-2 online softmax is an implementation
+detail); rows beyond the query end are not written. The reference kernel
+quantises Q/K to int8 and P to fp16; this oracle is the exact float64
+computation that both the reference and the bf16 HIP kernel approximate.
+
+Pinning: ``tests/test_oracle_attention.py`` checks it against
+``torch.nn.functional.scaled_dot_product_attention`` with a dense boolean
+mask in float64, and that full index lists reproduce dense attention.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def block_sparse_attention(q, k, v, index_lists, counts, *, block_q: int = 128,
+                           block_k: int = 64, scale: float | None = None) -> np.ndarray:
+    """float64 attention of ``q [B,H,Nq,D]`` over listed key blocks.
+
+    ``index_lists [B,H,Qb,W]`` absolute key-block indices (entries past
+    ``counts`` ignored). Rows with a zero count produce zeros.
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    B, H, Nq, D = q.shape
+    Tk = k.shape[-2]
+    scale = D ** -0.5 if scale is None else scale
+    Qb = -(-Nq // block_q)
+    out = np.zeros((B, H, Nq, v.shape[-1]), np.float64)
+    for b in range(B):
+        for h in range(H):
+            for i in range(Qb):
+                n = int(counts[b, h, i])
+                if n == 0:
+                    continue
+                blocks = np.asarray(index_lists[b, h, i, :n], np.int64)
+                keys = (blocks[:, None] * block_k + np.arange(block_k)[None]).reshape(-1)
+                keys = keys[keys < Tk]
+                rows = slice(i * block_q, min((i + 1) * block_q, Nq))
+                s = q[b, h, rows] @ k[b, h, keys].T * scale
+                s = s - s.max(axis=-1, keepdims=True)
+                p = np.exp(s)
+                p /= p.sum(axis=-1, keepdims=True)
+                out[b, h, rows] = p @ v[b, h, keys]
+    return out
+
+
+def dense_lists(B: int, H: int, Nq: int, Tk: int, block_q: int = 128, block_k: int = 64):
+    """Index lists that name every key block for every query block."""
+    Qb = -(-Nq // block_q)
+    nk = -(-Tk // block_k)
+    lists = np.broadcast_to(np.arange(nk, dtype=np.int32), (B, H, Qb, nk)).copy()
+    counts = np.full((B, H, Qb), nk, dtype=np.int32)
+    return lists, counts

@@ -1,0 +1,134 @@
+"""Kernel 2 (block selection + VASC ledger) vs the oracle: bit-exact.
+
+Index lists, counts, the execution priority and every ledger tensor (debt,
+pending arrival, QK-admission service, gate) must equal the oracle's bits
+when both start from the same float32 pooled scores and innovations.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import selector as OS
+
+pytestmark = pytest.mark.gpu
+
+TOPK, VASC = 0, 1
+
+
+def _softmax(x):
+    x = x - x.max(-1, keepdims=True)
+    e = np.exp(x)
+    return (e / e.sum(-1, keepdims=True)).astype(np.float32)
+
+
+def _scores(rng, shape, peak=1.0, levels=None):
+    logits = rng.standard_normal(shape) * peak
+    if levels:
+        logits = np.round(logits * levels) / levels  # forces exact ties
+    return _softmax(logits)
+
+
+def _bits(x):
+    return np.ascontiguousarray(np.asarray(x, np.float32)).view(np.uint32)
+
+
+def _assert_lists(out, sel, sink):
+    idx = out["index"].cpu().numpy()
+    cnt = out["count"].cpu().numpy()
+    K = sel.shape[-1]
+    assert np.array_equal(cnt, sel.sum(-1) + sink)
+    flat_i = idx.reshape(-1, idx.shape[-1])
+    flat_s = sel.reshape(-1, K)
+    for r in range(flat_s.shape[0]):
+        expect = np.concatenate([np.flatnonzero(flat_s[r]), K + np.arange(sink)])
+        got = flat_i[r, : expect.size]
+        assert np.array_equal(got, expect), f"row {r}: {got} != {expect}"
+
+
+@pytest.mark.parametrize("K,topk,force_last,sink,levels", [
+    (130, 32, False, 1, None), (130, 32, True, 1, 4), (7, 0, False, 0, 2), (518, 129, False, 3, 8),
+    (2072, 259, False, 10, None), (1, 1, False, 2, None), (31, 31, True, 0, 3), (64, 10, True, 4, 1),
+])
+def test_topk_lists_bit_exact(K, topk, force_last, sink, levels):
+    from vasc_amd import ops
+    rng = np.random.default_rng(K + topk)
+    score = _scores(rng, (1, 3, 17, K), levels=levels)
+    out = ops.select_blocks(torch.from_numpy(score).cuda(), mode=TOPK, topk=topk, force_last=force_last,
+                            sink_blocks=sink, want_mask=True)
+    sel = OS.topk_block_mask(score, 0, topk=topk)
+    if force_last:
+        sel[..., K - 1] = True
+    assert np.array_equal(out["mask"].cpu().numpy().astype(bool), sel)
+    _assert_lists(out, sel, sink)
+
+
+def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=False, levels=None):
+    from vasc_amd import ops
+    rng = np.random.default_rng(seed)
+    st = {}
+    debt = pending = service = None
+    gates = []
+    for layer in range(layers):
+        score = _scores(rng, (1, H, Q, K), peak=peak, levels=levels)
+        pv = rng.standard_normal((1, H, K, 64)).astype(np.float32)
+        iota = OS.innovation(pv)
+        if row_caps:
+            cap = rng.integers(0, K + 1, (1, H, Q))
+            prot = np.zeros((1, H, Q, K), bool)
+            prot[..., -1] = cap > 0
+            hint = None
+            M = int(cap.max())
+        else:
+            base = OS.topk_block_mask(score, 0, topk=topk)
+            if force_last:
+                base[..., K - 1] = True
+            cap = base.sum(-1)
+            prot = None
+            if force_last:
+                prot = np.zeros((1, H, Q, K), bool)
+                prot[..., K - 1] = True
+            hint = topk + int(force_last)
+            M = min(hint, K)
+        sel, info = OS.cosa_select(score, None, cap, layer_idx=layer, state=st, protected=prot,
+                                   max_capacity_hint=hint, iota=iota)
+        out = ops.select_blocks(
+            torch.from_numpy(score).cuda(), mode=VASC, topk=topk, innovation=torch.from_numpy(iota).cuda(),
+            row_cap=torch.from_numpy(cap.astype(np.int32)).cuda() if row_caps else None,
+            protected_mask=torch.from_numpy(prot).cuda() if (row_caps and prot is not None) else None,
+            force_last=force_last and not row_caps, max_capacity=M, sink_blocks=sink, debt=debt,
+            pending_arrival=pending, prev_service=service, want_priority=True, want_mask=True)
+        gate = int(out["gate"].item())
+        assert gate == int(info["gate"]), f"layer {layer}: gate {gate} != {info['gate']}"
+        gates.append(gate)
+        assert np.array_equal(_bits(out["priority"].cpu()), _bits(info["priority"])), f"layer {layer}: priority"
+        assert np.array_equal(out["mask"].cpu().numpy().astype(bool), sel), f"layer {layer}: support"
+        _assert_lists(out, sel, sink)
+        for key in ("debt", "arrival", "service"):
+            assert np.array_equal(_bits(out[key].cpu()), _bits(info[key])), f"layer {layer}: {key}"
+        debt, pending, service = out["debt"], out["arrival"], out["service"]
+    return gates
+
+
+@pytest.mark.parametrize("K,Q,force_last,peak,levels", [
+    (130, 65, True, 1.0, None), (7, 3, False, 3.0, None), (518, 40, False, 2.0, 4), (31, 9, True, 5.0, 2),
+])
+def test_vasc_chain_bit_exact(K, Q, force_last, peak, levels):
+    topk = max(int(K * 0.25), 1)
+    gates = _run_chain(K, Q, 4, 8, topk=topk, force_last=force_last, sink=1, peak=peak, seed=K, levels=levels)
+    assert any(gates[1:]) or True  # gate activity is data dependent; parity is the assertion
+
+
+def test_vasc_row_caps_and_protected_bit_exact():
+    """check_selector-style cases: random per-row capacity including 0."""
+    for K in (1, 2, 7, 8, 31):
+        _run_chain(K, 3, 2, 24, topk=1, force_last=False, sink=0, peak=1.0, seed=100 + K, row_caps=True)
+
+
+def test_vasc_c2_shape_chain():
+    """Config 2 shape: H=16, 259 query blocks x 518 key blocks, s=0.75, 3 layers."""
+    _run_chain(518, 259, 16, 3, topk=129, force_last=False, sink=3, peak=2.0, seed=2)
+
+
+def test_vasc_c3_shape_two_layers():
+    """Config 3 shape: H=16, 1036 x 2072 blocks at s=0.875 structural (224 blocks)."""
+    _run_chain(2072, 1036, 16, 2, topk=224, force_last=False, sink=10, peak=2.0, seed=3)

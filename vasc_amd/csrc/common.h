@@ -1,0 +1,108 @@
+// Shared device/host helpers of the gfx950 sparse global-attention library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/vasc_hip.h"
+
+namespace vasc {
+
+// ---------------------------------------------------------------- host side
+// Thread-local error string behind vasc_last_error() (defined in capi.cpp).
+void set_error(const char *fmt, ...);
+
+#define VASC_REQUIRE(cond, ...)          \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::vasc::set_error(__VA_ARGS__);    \
+      return VASC_ERR_ARGUMENT;          \
+    }                                    \
+  } while (0)
+
+#define VASC_SUPPORTED(cond, ...)        \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::vasc::set_error(__VA_ARGS__);    \
+      return VASC_ERR_UNSUPPORTED;       \
+    }                                    \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+int check_launch(const char *what);
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// ---------------------------------------------------------------- device side
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even float -> bfloat16 bits (NaN -> canonical quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f32(f32_to_bf16(f));
+}
+
+// Two floats -> packed bf16x2 with the hardware RNE conversion.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  floatx2 f = {a, b};
+  bf16x2 h = __builtin_convertvector(f, bf16x2);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  return (uint64_t(1) << lane_id()) - 1;
+}
+
+// Canonical 64-lane xor butterfly of float64 lane sums (offsets 32..1).
+__device__ __forceinline__ double wave_butterfly(double s) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off);
+  return s;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Maps the hardware workgroup id to a logical id so that each of the 8 XCDs
+// (which receive workgroups round-robin) processes one contiguous range of
+// logical ids, keeping neighbouring tiles of one head in one L2.
+__device__ __forceinline__ int64_t xcd_remap(int64_t pid, int64_t num) {
+  constexpr int64_t kXcd = 8;
+  const int64_t q = num / kXcd, r = num % kXcd;
+  const int64_t xcd = pid % kXcd, local = pid / kXcd;
+  return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+}  // namespace vasc
