@@ -1,0 +1,196 @@
+"""The drop-in operator API (vasc_amd.sparse_wrapper / attention) on the GPU.
+
+Covers the reference's own GPU smoke scenario (tests/gpu_smoke.py:14-42:
+topk and vasc x 3 layers, [1,2,512,64], s=0.75) and checks every API call
+against the oracle on the same inputs: masks and ledger bit-exact, attention
+within max-abs 2e-2 / mean-abs 2e-3.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import pooling as OP
+from oracle import selector as OS
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def release_env(request):
+    from vasc_amd.launcher import method_environment
+    saved = {k: v for k, v in os.environ.items() if k.startswith("SPARSE_VGGT_")}
+    for k in saved:
+        del os.environ[k]
+
+    def set_mode(model, mode):
+        for k in [k for k in os.environ if k.startswith("SPARSE_VGGT_")]:
+            del os.environ[k]
+        os.environ.update(method_environment(model, mode))
+
+    yield set_mode
+    for k in [k for k in os.environ if k.startswith("SPARSE_VGGT_")]:
+        del os.environ[k]
+    os.environ.update(saved)
+
+
+def _bits(t):
+    return np.ascontiguousarray(t.detach().float().cpu().numpy()).view(np.uint32)
+
+
+def test_reference_gpu_smoke_scenario(release_env):
+    from vasc_amd.attention import predict_attention
+    from vasc_amd.sparse_wrapper import block_sparse_attn_cuda
+    torch.manual_seed(0)
+    for mode in ("topk", "vasc"):
+        release_env("vggt", mode)
+        state = {}
+        for layer in range(3):
+            q, k, v = [torch.randn(1, 2, 512, 64, device="cuda", dtype=torch.float16) for _ in range(3)]
+            score = predict_attention(q, k)
+            out, sparsity = block_sparse_attn_cuda(q, k, v, score, sparse_ratio=.75, num_patch_tokens=512,
+                                                   layer_idx=layer, routing_state=state, return_sparsity=True)
+            assert out.shape == q.shape and out.dtype == q.dtype
+            assert torch.isfinite(out).all() and out.float().abs().sum() > 0
+            assert abs(float(sparsity) - 0.75) < 1e-6  # 2 of 8 blocks, no sink
+            # attention equals the oracle on the lists the selector produced
+            lists = OS.topk_block_mask(score.cpu().numpy(), 0, sparse_ratio=.75) if mode == "topk" else None
+            if lists is not None:
+                idx, cnt = OS.index_lists(lists)
+                ref = OA.block_sparse_attention(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                                v.float().cpu().numpy(), idx, cnt)
+                qb = q.to(torch.bfloat16).float().cpu().numpy()
+                ref_bf = OA.block_sparse_attention(qb, k.to(torch.bfloat16).float().cpu().numpy(),
+                                                   v.to(torch.bfloat16).float().cpu().numpy(), idx, cnt)
+                err = np.abs(out.float().cpu().numpy() - ref_bf)
+                assert err.max() <= 2e-2 and err.mean() <= 2e-3
+                assert np.abs(ref - ref_bf).max() < 5e-2
+        if mode == "vasc":
+            assert state["cosa_value_risk_pair_pending_layer"] == 2
+
+
+def test_predict_attention_matches_oracle():
+    from vasc_amd.attention import predict_attention
+    g = torch.Generator().manual_seed(1)
+    q = (torch.randn(1, 3, 1000, 64, generator=g) * 2).to(torch.bfloat16)
+    k = (torch.randn(1, 3, 1041, 64, generator=g) * 2).to(torch.bfloat16)
+    p = predict_attention(q.cuda(), k.cuda()).cpu().numpy()
+    ref, _, _ = OP.pooled_prob(q.float().numpy(), k.float().numpy(), bf16=True)
+    assert p.shape == ref.shape
+    assert np.isclose(p, ref, rtol=1e-4, atol=1e-9).mean() > 0.999
+
+
+def test_get_block_mask_bit_exact():
+    from vasc_amd.sparse_wrapper import get_block_mask
+    rng = np.random.default_rng(2)
+    s = rng.integers(0, 5, (1, 4, 65, 130)).astype(np.float32) / 4  # heavy ties
+    m = get_block_mask(torch.from_numpy(s).cuda(), 1, sparse_ratio=0.75).cpu().numpy()
+    assert np.array_equal(m, OS.topk_block_mask(s, 1, sparse_ratio=0.75))
+    m = get_block_mask(torch.from_numpy(s).cuda(), 0, topk=0).cpu().numpy()
+    assert np.array_equal(m, OS.topk_block_mask(s, 0, topk=0))
+
+
+def test_cosa_mask_api_chain_bit_exact():
+    from vasc_amd import sparse_wrapper as SW
+    rng = np.random.default_rng(3)
+    st_gpu, st_ref = {}, {}
+    B, H, Q, K = 1, 2, 9, 31
+    for layer in range(6):
+        x = rng.standard_normal((B, H, Q, K))
+        s = (np.exp(x) / np.exp(x).sum(-1, keepdims=True)).astype(np.float32)
+        pv = rng.standard_normal((B, H, K, 64)).astype(np.float32)
+        cap = rng.integers(0, K + 1, (B, H, Q))
+        base = np.arange(K) < cap[..., None]
+        prot = np.zeros_like(base)
+        prot[..., -1] = cap > 0
+        got = SW.get_cosa_value_risk_pair_debt_mask(
+            torch.from_numpy(s).cuda(), torch.from_numpy(pv).cuda(), torch.from_numpy(base).cuda(),
+            layer_idx=layer, routing_state=st_gpu, protected_mask=torch.from_numpy(prot).cuda(),
+            fp32_projection=True)
+        ref, info = OS.cosa_select(s, pv, cap, layer_idx=layer, state=st_ref, protected=prot)
+        assert np.array_equal(got.cpu().numpy(), ref)
+        assert np.array_equal(_bits(st_gpu[SW.STATE_KEY]), np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
+        assert np.array_equal(_bits(st_gpu[SW.PENDING_KEY]), st_ref[OS.PENDING_KEY].view(np.uint32))
+        assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_priority"]), info["priority"].view(np.uint32))
+    t_gpu = SW.finalize_cosa_value_risk_pair_debt(st_gpu)
+    t_ref = OS.finalize(st_ref)
+    assert t_gpu and t_ref and SW.finalize_cosa_value_risk_pair_debt(st_gpu) == {}
+    assert np.array_equal(_bits(st_gpu[SW.STATE_KEY]), np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("model", ["vggt", "pi3"])
+def test_block_sparse_attn_c1_end_to_end(release_env, model):
+    """Config 1 (8 frames x 1041 tokens, H=16) through block_sparse_attn_cuda in
+    vasc mode, two chained layers; VGGT uses the official mask (no forced
+    tail), Pi3 protects the mixed tail block."""
+    from vasc_amd.attention import predict_attention
+    from vasc_amd.sparse_wrapper import block_sparse_attn_cuda
+    release_env(model, "vasc")
+    N, P, S, H, D = 8, 1041, 5, 16, 64
+    Np, Tk = N * (P - S), N * P
+    g = torch.Generator().manual_seed(4)
+    st_gpu, st_ref = {}, {}
+    for layer in range(2):
+        q = torch.randn(1, H, Np, D, generator=g).to(torch.bfloat16)
+        k = torch.randn(1, H, Tk, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, H, Tk, D, generator=g).to(torch.bfloat16)
+        qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+        score = predict_attention(qc, kc[:, :, :Np])
+        out, sparsity = block_sparse_attn_cuda(qc, kc, vc, score, sparse_ratio=0.75, return_sparsity=True,
+                                               layer_idx=layer, routing_state=st_gpu, num_patch_tokens=Np)
+        from vasc_amd import ops
+        _, _, _, iota = ops.pool_qkv(v=vc[:, :, :Np])
+        final, _ = OS.layer_selection(score.cpu().numpy(), mode="vasc", sparse_ratio=0.75, patch_tokens=Np,
+                                      total_tokens=Tk, official_mask=(model == "vggt"), state=st_ref,
+                                      layer_idx=layer, iota=iota.cpu().numpy())
+        idx, cnt = OS.index_lists(final)
+        assert abs(float(sparsity) - (1 - final.mean())) < 1e-6
+        ref = OA.block_sparse_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), idx, cnt)
+        err = np.abs(out.float().cpu().numpy() - ref)
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
+        assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_debt"]),
+                              np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
+
+
+def test_global_layer_forward_dense_limit():
+    """adaptive_sparse_attention_forward at sparsity 0 equals dense attention of
+    the same module (all key blocks kept)."""
+    from vasc_amd.attention import adaptive_sparse_attention_forward
+
+    class Attn(torch.nn.Module):
+        def __init__(self, dim, heads):
+            super().__init__()
+            self.qkv = torch.nn.Linear(dim, 3 * dim)
+            self.proj = torch.nn.Linear(dim, dim)
+            self.q_norm = torch.nn.LayerNorm(dim // heads)
+            self.k_norm = torch.nn.LayerNorm(dim // heads)
+            self.rope = None
+            self.heads = heads
+
+    torch.manual_seed(5)
+    N, Hp, Wp, S, heads, dim = 3, 10, 12, 5, 4, 256
+    P = Hp * Wp + S
+    m = Attn(dim, heads).cuda().to(torch.bfloat16)
+    x = torch.randn(1, N * P, dim, device="cuda", dtype=torch.bfloat16)
+    ys, xs = torch.meshgrid(torch.arange(Hp), torch.arange(Wp), indexing="ij")
+    patch_pos = torch.stack([ys.reshape(-1), xs.reshape(-1)], -1) + 1
+    pos = torch.cat([torch.zeros(S, 2, dtype=torch.long), patch_pos]).expand(N, P, 2).cuda()
+    saved = {k: os.environ.pop(k) for k in list(os.environ) if k.startswith("SPARSE_VGGT_")}
+    try:
+        os.environ["SPARSE_VGGT_OFFICIAL_MASK"] = "1"
+        out = adaptive_sparse_attention_forward(m, x, pos, sparse_ratio=0.0, num_special_tokens=S, num_heads=heads,
+                                                routing_state={})
+    finally:
+        os.environ.pop("SPARSE_VGGT_OFFICIAL_MASK", None)
+        os.environ.update(saved)
+    with torch.no_grad():
+        qkv = m.qkv(x).float().reshape(1, N * P, 3, heads, dim // heads).permute(2, 0, 3, 1, 4)
+        q, k, v = qkv.unbind(0)
+        q, k = m.q_norm(q.to(torch.bfloat16)).float(), m.k_norm(k.to(torch.bfloat16)).float()
+        ref = torch.nn.functional.scaled_dot_product_attention(q, k, v)
+        ref = m.proj(ref.transpose(1, 2).reshape(1, N * P, dim).to(torch.bfloat16))
+    err = (out.float() - ref.float()).abs()
+    assert err.max() < 6e-2 and err.mean() < 6e-3, (err.max().item(), err.mean().item())

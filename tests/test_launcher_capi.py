@@ -1,0 +1,91 @@
+"""Host-side logic: the launcher mirror and the C-ABI library surface (CPU only)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from oracle import profile as PR
+from vasc_amd import _lib, launcher
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+# ------------------------------------------------------------------ launcher
+def test_layer_sparsity_matches_oracle_and_string_form():
+    for model in ("vggt", "pi3"):
+        for s in (0.55, 0.65, 0.75, 0.85, 0.875):
+            assert launcher.layer_sparsity(model, s) == PR.layer_sparsity(model, s)
+        text = launcher.layer_sparsity_string(model, 0.75, "paper")
+        assert all(len(x.split(".")[1]) == 10 for x in text.split(","))
+
+
+def test_method_environment_release_matrix():
+    for model in ("vggt", "pi3"):
+        for mode in launcher.MODES:
+            env = launcher.method_environment(model, mode)
+            assert env["SPARSE_VGGT_QK_PV_THRESHOLD"] == "1e10"
+            assert env["SPARSE_VGGT_SKIP_ROUTING_STATS"] == "1"
+            assert env["SPARSE_VGGT_COSA_VALUE_RISK_PAIR_DEBT"] == str(int(mode == "vasc"))
+            assert ("SPARSE_VGGT_OFFICIAL_MASK" in env) == (model == "vggt" and mode != "dense")
+    with pytest.raises(ValueError):
+        launcher.method_environment("vggt", "other")
+
+
+def test_routing_config_resolves_release_modes():
+    for model in ("vggt", "pi3"):
+        for mode in ("topk", "vasc"):
+            cfg = launcher.routing_config(launcher.method_environment(model, mode))
+            assert cfg.mode == mode
+            assert cfg.official_mask == (model == "vggt")
+            assert cfg.skip_routing_stats
+
+
+def test_routing_config_rejects_research_switches():
+    env = launcher.method_environment("vggt", "vasc")
+    for extra in ({"SPARSE_VGGT_COSA_ORDERED_LUT": "1"}, {"SPARSE_VGGT_QK_PV_THRESHOLD": "sequence_mass_bound"},
+                  {"SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN": "pv_execution"}):
+        with pytest.raises(NotImplementedError):
+            launcher.routing_config({**env, **extra})
+
+
+def test_allocation_settings():
+    a = launcher.allocation_settings("vggt", "vasc", 0.75, True)
+    assert a["applied"] and a["effective_policy"] == "paper" and len(a["layer_sparsities"]) == 24
+    d = launcher.allocation_settings("vggt", "dense", 0.75, True)
+    assert not d["applied"] and d["layer_sparsities"] == [0.0] * 24
+    u = launcher.allocation_settings("pi3", "topk", 0.65, True)
+    assert u["effective_policy"] == "uniform" and u["layer_sparsities"] == [0.65] * 18
+
+
+# ------------------------------------------------------------------ C-ABI
+def _header_functions():
+    text = (ROOT / "include" / "vasc_hip.h").read_text()
+    return set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(vasc_\w+)\s*\(", text, flags=re.M))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _header_functions()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), name
+    assert names == set(_lib.SIGNATURES), "ctypes table out of sync with include/vasc_hip.h"
+    assert lib.vasc_abi_version() == 1
+
+
+def test_host_only_queries_and_argument_errors():
+    lib = _lib.load()
+    assert lib.vasc_select_workspace_size(1, 16, 259, 518) > 16 * 259 * 259 * 4
+    assert lib.vasc_select_workspace_size(0, 16, 259, 518) == 0
+    assert lib.vasc_packed_v_elems(1, 16, 33312, 64) == 16 * 521 * 64 * 64
+    # validation happens before any HIP call: these return without a GPU
+    rc = lib.vasc_pack_v(None, 0, 0, 8, 1, 1, 64, 64, None, None)
+    assert rc == 1 and b"required" in lib.vasc_last_error()
+    rc = lib.vasc_pack_v(None, 0, 0, 8, 1, 1, 64, 128, None, None)
+    assert rc == 2 and b"head_dim" in lib.vasc_last_error()
+    rc = lib.vasc_block_sparse_attn_fwd(None, 0, 0, 8, None, 0, 0, 8, None, None, 0, 0, 8, 1, 1, 128, 64, 64,
+                                        None, 1, None, 0, ctypes.c_float(0.125), None)
+    assert rc == 1
+    with pytest.raises(_lib.VascArgumentError):
+        _lib.call("vasc_settle_terminal", None, None, None, 0, None, None)

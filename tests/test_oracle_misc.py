@@ -1,0 +1,126 @@
+"""Pins of the oracle's pooling, LUT, attention, profile and CPU baseline."""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import cpu_baseline as CB
+from oracle import lut as OL
+from oracle import pooling as OP
+from oracle import profile as PR
+from oracle import selector as OS
+
+
+# ------------------------------------------------------------------ pooling
+def test_pool_blocks_exact_means_and_tail():
+    rng = np.random.default_rng(0)
+    x = rng.integers(-50, 50, (1, 1, 150, 3)).astype(np.float32) / 8
+    out = OP.pool_blocks(x, 64)
+    assert out.shape == (1, 1, 3, 3)
+    for b, (lo, hi) in enumerate(((0, 64), (64, 128), (128, 150))):
+        for d in range(3):
+            exact = sum(Fraction(float(v)) for v in x[0, 0, lo:hi, d]) / (hi - lo)
+            assert out[0, 0, b, d] == np.float32(float(exact))
+
+
+def test_pool_blocks_matches_torch_avg_pool_ceil_mode():
+    x = torch.randn(2, 3, 777, 64)
+    ours = OP.pool_blocks(x.numpy(), 128)
+    ref = torch.nn.functional.avg_pool1d(x.reshape(6, 777, 64).transpose(1, 2), 128, ceil_mode=True)
+    np.testing.assert_allclose(ours, ref.transpose(1, 2).reshape(2, 3, -1, 64).numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_bf16_round_matches_torch():
+    x = torch.randn(10000) * 10 ** torch.randint(-20, 20, (10000,)).float()
+    np.testing.assert_array_equal(OP.bf16_round(x.numpy()), x.to(torch.bfloat16).float().numpy())
+
+
+def test_softmax_rows_sum_to_one():
+    p = OP.softmax(np.random.default_rng(1).standard_normal((4, 9)) * 30)
+    np.testing.assert_allclose(p.sum(-1), 1.0, rtol=1e-6)
+
+
+# ------------------------------------------------------------------ LUT
+def test_lut_encode_matches_reference_restatement_and_round_trips():
+    rng = np.random.default_rng(2)
+    m = rng.random((2, 3, 7, 40)) < 0.3
+    m[0, 0, 0] = False
+    m[0, 0, 1] = True
+    lut, cnt = OL.encode(m)
+    ref_lut, ref_cnt = OL.reference_block_map_lut(m)
+    assert np.array_equal(cnt, ref_cnt)
+    for idx in np.ndindex(m.shape[:-1]):
+        c = cnt[idx]
+        assert np.array_equal(lut[idx][:c], ref_lut[idx][:c])
+        assert not lut[idx][c:].any()
+    assert np.array_equal(OL.decode(lut, cnt), m)
+
+
+# ------------------------------------------------------------------ attention
+def test_block_sparse_attention_matches_masked_sdpa():
+    rng = np.random.default_rng(3)
+    B, H, Nq, Tk, D = 1, 2, 300, 230, 16
+    q, k, v = (rng.standard_normal((B, H, n, D)) for n in (Nq, Tk, Tk))
+    qb, kb = 3, 4
+    mask_blocks = rng.random((B, H, qb, kb)) < 0.5
+    mask_blocks[..., 0] = True
+    idx, cnt = OS.index_lists(mask_blocks)
+    out = OA.block_sparse_attention(q, k, v, idx, cnt)
+    full = np.repeat(np.repeat(mask_blocks, 128, axis=2), 64, axis=3)[:, :, :Nq, :Tk]
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        *(torch.from_numpy(t) for t in (q, k, v)), attn_mask=torch.from_numpy(full))
+    np.testing.assert_allclose(out, ref.numpy(), atol=1e-10)
+
+
+def test_dense_lists_equal_unmasked_attention():
+    rng = np.random.default_rng(4)
+    q, k, v = (rng.standard_normal((1, 1, n, 8)) for n in (200, 150, 150))
+    idx, cnt = OA.dense_lists(1, 1, 200, 150)
+    out = OA.block_sparse_attention(q, k, v, idx, cnt)
+    ref = torch.nn.functional.scaled_dot_product_attention(*(torch.from_numpy(t) for t in (q, k, v)))
+    np.testing.assert_allclose(out, ref.numpy(), atol=1e-10)
+
+
+# ------------------------------------------------------------------ profile
+def test_structural_profile_matches_release_assertions():
+    """The reference's tests/test_release.py:43-51, 109-121."""
+    for model, count, low in (("vggt", 24, 11), ("pi3", 18, 12)):
+        for s in (.75, .85):
+            vals = PR.layer_sparsity(model, s)
+            assert len(vals) == count
+            assert abs(sum(vals) / count - s) < 1e-9
+            assert abs(vals[low] - (s - .05)) < 1e-9
+        assert PR.layer_sparsity(model, .65) is None
+        assert PR.layer_sparsity(model, .70) is None
+        assert PR.layer_sparsity(model, .7001) is not None
+        assert PR.layer_sparsity(model, .85, "uniform") is None
+        with pytest.raises(ValueError):
+            PR.layer_sparsity(model, .99)
+
+
+def test_budget_table_of_the_survey():
+    c2 = PR.layer_sparsity("vggt", .75)
+    assert {PR.budget(518, s) for s in c2} == {155, 120}
+    c3 = PR.layer_sparsity("vggt", .875)
+    assert {PR.budget(2072, s) for s in c3} == {362, 224}
+    c4 = PR.layer_sparsity("pi3", .75)
+    assert {PR.budget(1036, s) for s in c4} == {310, 233}
+    assert PR.budget(130, .75) == 32 and PR.budget(518, .75) == 129
+
+
+# ------------------------------------------------------------------ CPU baseline
+def test_cpu_baseline_matches_float64_oracle():
+    g = torch.Generator().manual_seed(5)
+    Np, Tk, H, D = 500, 520, 2, 64
+    q = torch.randn(1, H, Np, D, generator=g)
+    k = torch.randn(1, H, Tk, D, generator=g)
+    v = torch.randn(1, H, Tk, D, generator=g)
+    out = CB.topk_layer(q, k, v, 0.75)
+    prob = CB.pooled_prob(q, k[..., :Np, :])
+    sink = -(-Tk // 64) - prob.shape[-1]
+    final = OS.topk_block_mask(prob.numpy(), sink, sparse_ratio=0.75)
+    idx, cnt = OS.index_lists(final)
+    ref = OA.block_sparse_attention(q.double().numpy(), k.double().numpy(), v.double().numpy(), idx, cnt)
+    np.testing.assert_allclose(out.numpy(), ref, atol=2e-5)

@@ -1,0 +1,149 @@
+"""Pins of oracle/selector.py beyond the golden vectors: the reference's
+check_selector invariants and closed forms that fix the arithmetic."""
+import itertools
+
+import numpy as np
+import pytest
+
+from oracle import selector as OS
+
+
+def _softmax(x):
+    e = np.exp(x - x.max(-1, keepdims=True))
+    return (e / e.sum(-1, keepdims=True)).astype(np.float32)
+
+
+def test_select_top_matches_brute_force_with_lower_index_ties():
+    rng = np.random.default_rng(0)
+    for K in range(1, 7):
+        for _ in range(30):
+            prio = rng.integers(0, 3, K).astype(np.float32)  # many exact ties
+            for c in range(K + 1):
+                got = OS.select_top(prio, np.array(c))
+                # brute force: among all subsets of size c, the lexicographically best
+                # (sorted priorities descending, then smallest indices)
+                best = None
+                for sub in itertools.combinations(range(K), c):
+                    key = (sorted(prio[list(sub)], reverse=True), [-i for i in sub])
+                    if best is None or key > best[0]:
+                        best = (key, sub)
+                expect = np.zeros(K, bool)
+                expect[list(best[1])] = True
+                assert np.array_equal(got, expect), (prio, c)
+
+
+def test_check_selector_invariants():
+    """tests/check_selector.py:44-65 of the reference, on the oracle."""
+    rng = np.random.default_rng(20260906)
+    active = 0
+    for K in (1, 2, 7, 8, 31):
+        for protect in (False, True):
+            st = {}
+            for layer in range(24):
+                scores = _softmax(rng.standard_normal((1, 2, 3, K)))
+                values = rng.standard_normal((1, 2, K, 13)).astype(np.float32)
+                cap = rng.integers(0, K + 1, (1, 2, 3))
+                prot = np.zeros((1, 2, 3, K), bool)
+                if protect:
+                    prot[..., -1] = cap > 0
+                sel, info = OS.cosa_select(scores, values, cap, layer_idx=layer, state=st, protected=prot)
+                assert np.array_equal(sel.sum(-1), cap)
+                assert sel[prot].all()
+                assert np.isfinite(st["cosa_value_risk_pair_priority"]).all()
+                active += bool((st[OS.STATE_KEY] > 0).any())
+            assert OS.finalize(st)
+            assert OS.finalize(st) == {}
+    assert active > 0
+
+
+def test_layer0_priority_is_conservative_arrival():
+    rng = np.random.default_rng(1)
+    s = _softmax(rng.standard_normal((1, 3, 5, 20)))
+    v = rng.standard_normal((1, 3, 20, 64)).astype(np.float32)
+    sel, info = OS.cosa_select(s, v, np.full((1, 3, 5), 6), layer_idx=0, state={})
+    assert not info["gate"]
+    A, _, _, _ = OS.conservative_arrival(s, OS.innovation(v), np.full((1, 3, 5), 6))
+    assert np.array_equal(info["priority"], A)
+    # closed form of the conservative projection on one row
+    iota_k = np.repeat(OS.innovation(v), 2, axis=-1)
+    risk = s[0, 0, 0].astype(np.float64) * iota_k[0, 0]
+    closed = np.clip(risk * 6 / risk.sum(), 0, 1)
+    np.testing.assert_allclose(A[0, 0, 0], closed, rtol=1e-5)
+
+
+def test_uniform_innovation_unsaturated_reduces_to_topk():
+    rng = np.random.default_rng(2)
+    K = 40
+    s = _softmax(0.1 * rng.standard_normal((1, 2, 7, K)))  # flat: cap * share < 1 everywhere
+    v = np.zeros((1, 2, K, 64), np.float32)
+    v[:, :, 1::2, :] = 1.0  # every pair differs by the same amount
+    iota = OS.innovation(v)
+    assert np.all(iota == iota.flat[0]) and iota.flat[0] > 0
+    cap = np.full((1, 2, 7), 10)
+    sel, info = OS.cosa_select(s, v, cap, layer_idx=0, state={})
+    assert info["priority"].max() < 1
+    assert np.array_equal(sel, OS.select_top(s, cap))
+
+
+def test_zero_innovation_selects_first_blocks():
+    s = _softmax(np.random.default_rng(3).standard_normal((1, 1, 4, 12)))
+    v = np.ones((1, 1, 12, 64), np.float32)
+    sel, info = OS.cosa_select(s, v, np.full((1, 1, 4), 5), layer_idx=0, state={})
+    assert np.all(info["priority"] == 0)
+    assert np.array_equal(sel[0, 0], np.tile(np.arange(12) < 5, (4, 1)))
+
+
+def test_zero_debt_keeps_gate_closed_and_settlement_conserves():
+    rng = np.random.default_rng(4)
+    K, Q = 16, 6
+    st = {}
+    for layer in range(3):
+        s = _softmax(rng.standard_normal((1, 2, Q, K)))
+        v = rng.standard_normal((1, 2, K, 64)).astype(np.float32)
+        prev_debt = st.get(OS.STATE_KEY)
+        pending = st.get(OS.PENDING_KEY)
+        service = None if pending is None else st[OS.SERVICE_KEY]["pair_service_fraction"]
+        sel, info = OS.cosa_select(s, v, np.full((1, 2, Q), 5), layer_idx=layer, state=st)
+        if layer == 0:
+            assert not info["gate"] and np.all(info["debt"] == 0)
+        else:
+            d0 = np.zeros_like(pending) if prev_debt is None else prev_debt
+            # D' - D - A + S - refl == 0 up to one float32 rounding per term
+            resid = info["debt"].reshape(d0.shape) - d0 - pending + service - info["reflection"].reshape(d0.shape)
+            assert np.abs(resid).max() <= 4 * np.finfo(np.float32).eps
+        # service counts every selected child once: sum(service*pair_size*Q) == selected blocks
+        ps = np.where(np.arange((K + 1) // 2) == (K + 1) // 2 - 1, 1 + (K % 2 == 0), 2)
+        assert np.isclose((info["service"] * ps * Q).sum(), sel.sum())
+
+
+def test_gate_rule_examples():
+    serv = np.array([[[0.5, 0.5]]], np.float32)
+    assert OS.service_gate(serv, np.zeros_like(serv))          # nothing wasted
+    assert not OS.service_gate(np.zeros_like(serv), np.zeros_like(serv))  # no service at all
+    refl = np.array([[[0.5, 0.5]]], np.float32)
+    assert not OS.service_gate(serv, refl + 0.1)               # waste exceeds useful repayment
+
+
+def test_topk_block_mask_sink_and_min_one():
+    s = _softmax(np.random.default_rng(5).standard_normal((1, 2, 3, 9)))
+    m = OS.topk_block_mask(s, 2, sparse_ratio=0.99)  # int(9*0.01) = 0 -> fill rule keeps 1
+    assert np.array_equal(m[..., :9].sum(-1), np.ones((1, 2, 3)))
+    assert m[..., 9:].all()
+    assert np.array_equal(m[..., :9].argmax(-1), s.argmax(-1))
+
+
+@pytest.mark.parametrize("official", [True, False])
+def test_layer_selection_mixed_tail(official):
+    # C1 geometry: 8288 patch tokens -> 130 key blocks, the last holding 32 patch tokens
+    s = _softmax(np.random.default_rng(6).standard_normal((1, 2, 65, 130)))
+    final, _ = OS.layer_selection(s, mode="topk", sparse_ratio=0.75, patch_tokens=8288, total_tokens=8328,
+                                  official_mask=official)
+    assert final.shape[-1] == 131 and final[..., 130].all()
+    assert final[..., 129].all() == (not official)
+    st = {}
+    final_v, info = OS.layer_selection(s, mode="vasc", sparse_ratio=0.75, patch_tokens=8288, total_tokens=8328,
+                                       official_mask=official, state=st, layer_idx=0,
+                                       pooled_value=np.random.default_rng(7).standard_normal((1, 2, 130, 64)))
+    assert np.array_equal(final_v[..., :130].sum(-1), final[..., :130].sum(-1))
+    if not official:
+        assert final_v[..., 129].all()

@@ -1,0 +1,349 @@
+"""Drop-in sparse-attention operator API (GPU only).
+
+Mirrors the operator surface of the reference's
+``src/sparse_vggt/utils/sparse_wrapper.py`` (``SW``) for the release modes:
+
+* ``check_sparse_mode`` / ``check_sparse_mode_three_type`` (SW:1143-1196)
+* ``get_block_mask`` (SW:1199-1268), ties to the lower block index
+* ``get_cosa_value_risk_pair_debt_mask`` (SW:3632-4098) and
+  ``finalize_cosa_value_risk_pair_debt`` (SW:4101-4177) on the same
+  ``routing_state`` dict keys
+* ``block_sparse_attn_cuda`` (SW:6868-8245): selection by the environment's
+  mode switch (``vasc``/``topk``), mixed-tail and sink rules, V pack and the
+  bf16 MFMA block-sparse attention kernel
+* ``block_map_lut`` (``spas_sage_attn/utils.py:54-87``) and its inverse
+
+Every function runs the HIP kernels of ``libvasc_hip.so``; CPU tensors are
+rejected. Documented differences from the reference: attention computes in
+bf16 with fp32 accumulation (the reference quantises Q/K to int8 and P to
+fp16); ``routing_state["cosa_value_risk_pair_selected_indices"]`` holds the
+ascending index lists (the reference stores them in priority order); ties in
+the selection go to the lower block index (``torch.topk`` leaves them
+unspecified).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib, ops
+from .launcher import routing_config
+
+KBLK = 64
+STATE_KEY = "cosa_value_risk_pair_debt"
+PENDING_KEY = "cosa_value_risk_pair_pending_arrival"
+PENDING_LAYER_KEY = "cosa_value_risk_pair_pending_layer"
+SERVICE_KEY = "qk_pv_service_observation"
+
+# Research keyword arguments of block_sparse_attn_cuda (SW:6868-6971) with the
+# values the release modes pass; any other value selects a research router
+# that this build does not implement.
+_RESEARCH_DEFAULTS = {
+    "use_radial_layerwise": False, "num_frames": None, "tokens_per_frame": None, "decay_factor": 1.0,
+    "dense_neighbor": 1, "layer_sparsity_ratios": None, "use_distance_routed": False,
+    "route_frame_threshold": 4, "use_covariance_aware_importance": False, "covariance_weight": 0.5,
+    "covariance_eps": 1e-8, "key_block_variance": None, "use_adaptive_slit_routing": False,
+    "adaptive_slit_temporal_window": 10, "adaptive_slit_stable_quantile": 0.6,
+    "adaptive_slit_change_quantile": 0.7, "adaptive_slit_narrow_width": 1, "adaptive_slit_base_width": 2,
+    "adaptive_slit_expand_width": 4, "use_soft_geometry_routing": False, "use_preview_adaptive_routing": False,
+    "use_dual_path_routing": False, "use_layerwise_hybrid_routing": False,
+    "use_local_layerwise_hybrid_routing": False, "use_coverage_layerwise_routing": False,
+    "use_persistent_view_graph_routing": False, "analyze_importance_blocks": False,
+    "analyze_block_selection": False,
+}
+# Routing knobs that only matter when their router is enabled above.
+_INERT_WITHOUT_ROUTER = ("preview_", "dual_path_", "hybrid_", "mid_frame_", "view_graph_", "core_frame_",
+                         "transition_frame_", "geometry_", "decay_gamma", "frame_normalize", "distance_calibrate",
+                         "entropy_adaptive", "head_adaptive")
+
+
+def check_sparse_mode(sparse_ratio, cdf_threshold):
+    """Exactly one of: ratio, cdf, ratio + cdf (SW:1143-1166)."""
+    use_ratio, use_cdf = sparse_ratio is not None, cdf_threshold is not None
+    assert (use_ratio and not use_cdf) + (use_cdf and not use_ratio) + (use_ratio and use_cdf) == 1, \
+        f"Current: {sparse_ratio=}, {cdf_threshold=}"
+
+
+def check_sparse_mode_three_type(topk, sparse_ratio, cdf_threshold):
+    """Exactly one of: topk, ratio, cdf, ratio + cdf (SW:1169-1196)."""
+    t, r, c = topk is not None, sparse_ratio is not None, cdf_threshold is not None
+    modes = (t and not r and not c) + (not t and r and not c) + (not t and not r and c) + (r and c and not t)
+    assert modes == 1, f"Current: {topk=}, {sparse_ratio=}, {cdf_threshold=}"
+
+
+def _require_gpu(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (this operator has no CPU path)")
+
+
+def _budget(key_blocks: int, topk, sparse_ratio, cdf_threshold) -> int:
+    check_sparse_mode_three_type(topk, sparse_ratio, cdf_threshold)
+    if cdf_threshold is not None:
+        raise NotImplementedError("cdf_threshold selection is not built; use sparse_ratio or topk")
+    if sparse_ratio is not None:
+        assert 0 <= sparse_ratio <= 1
+        topk = int(key_blocks * (1 - sparse_ratio))
+    assert 0 <= topk <= key_blocks
+    return int(topk)
+
+
+def get_block_mask(pooled_score: torch.Tensor, sink_blocks: int, topk: int | None = None,
+                   sparse_ratio: float | None = None, cdf_threshold: float | None = None,
+                   eps: float = 1e-5) -> torch.Tensor:
+    """Top-k block map with ``sink_blocks`` trailing always-on columns.
+
+    Returns bool ``[B,H,Q,K+sink]`` with ``max(topk,1)`` patch blocks per row.
+    """
+    _require_gpu(pooled_score, "pooled_score")
+    B, H, Q, K = pooled_score.shape
+    assert 0 <= sink_blocks <= K
+    t = _budget(K, topk, sparse_ratio, cdf_threshold)
+    out = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=t, want_mask=True)
+    mask = out["mask"].bool()
+    if sink_blocks > 0:
+        mask = torch.cat([mask, mask.new_ones(B, H, Q, sink_blocks)], dim=-1)
+    return mask
+
+
+def block_map_lut(block_map: torch.Tensor):
+    """Delta-encoded LUT and counts of a bool block map (utils.py:54-87)."""
+    m = block_map.bool()
+    K = m.shape[-1]
+    pos = torch.arange(K, device=m.device, dtype=torch.int32).expand_as(m)
+    key = torch.where(m, pos, torch.full_like(pos, K))
+    idx = torch.sort(key, dim=-1).values
+    count = m.sum(-1, dtype=torch.int32)
+    delta = torch.diff(idx, dim=-1, prepend=torch.zeros_like(idx[..., :1]))
+    valid = torch.arange(K, device=m.device).view(*([1] * (m.dim() - 1)), K) < count.unsqueeze(-1)
+    return torch.where(valid, delta, torch.zeros_like(delta)).to(torch.int32), count
+
+
+def _ledger_inputs(routing_state: dict, B: int, H: int, P: int):
+    """Debt, pending arrival and service of the previous layer (SW:3793-3832)."""
+    shape = (B, H, 1, P)
+    prev = routing_state.get(STATE_KEY)
+    debt = prev if (prev is not None and tuple(prev.shape) == shape) else None
+    pending = routing_state.get(PENDING_KEY)
+    obs = routing_state.pop(SERVICE_KEY, None)
+    service = None
+    if pending is not None:
+        if obs is None or not obs.get("identity_observed", False):
+            raise RuntimeError("CoSA pair debt requires exact PV service identity")
+        if obs.get("layer_idx") != routing_state.get(PENDING_LAYER_KEY):
+            raise RuntimeError("PV service does not match pending CoSA layer")
+        if "pair_service_fraction" not in obs:
+            raise NotImplementedError("only the qk_admission service domain is built")
+        service = obs["pair_service_fraction"]
+        if tuple(service.shape) != shape:
+            raise RuntimeError("PV service changed the stable pair layout")
+        if tuple(pending.shape) != shape:
+            raise RuntimeError("pending arrival changed the stable pair layout")
+    return debt, pending, service
+
+
+def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_idx: int, M: int) -> None:
+    B, H, Q, K = score.shape
+    P = (K + 1) // 2
+    routing_state[STATE_KEY] = out["debt"].view(B, H, 1, P)
+    routing_state[PENDING_KEY] = out["arrival"].view(B, H, 1, P)
+    routing_state[PENDING_LAYER_KEY] = int(layer_idx)
+    routing_state[SERVICE_KEY] = {
+        "layer_idx": int(layer_idx),
+        "identity_observed": True,
+        "service_domain": "qk_admission",
+        "pair_service_fraction": out["service"].view(B, H, 1, P),
+    }
+    if "priority" in out:
+        routing_state["cosa_value_risk_pair_priority"] = out["priority"]
+    routing_state["cosa_value_risk_pair_max_patch_blocks"] = int(M)
+    routing_state["cosa_value_risk_pair_selected_indices"] = out["index"][..., :M]
+    routing_state["cosa_value_risk_pair_qk_order_priority"] = score.float().clamp_min(0.0).nan_to_num(nan=0.0)
+
+
+def _stats(out: dict, cap: torch.Tensor | None) -> dict:
+    stats = {
+        "cosa_pair_debt_enabled": torch.ones((), device=out["debt"].device),
+        "cosa_pair_service_gate_debt": out["gate"].float().view(()),
+        "cosa_pair_arrival": out["arrival"].sum(-1).mean(),
+        "cosa_pair_backlog": out["debt"].sum(-1).mean(),
+    }
+    if cap is not None:
+        stats["cosa_pair_qk_capacity"] = cap.float().mean()
+    return stats
+
+
+def get_cosa_value_risk_pair_debt_mask(pooled_score: torch.Tensor, pooled_value: torch.Tensor | None,
+                                       base_mask: torch.Tensor, *, layer_idx: int, routing_state: dict | None,
+                                       stats_store: dict | None = None, protected_mask: torch.Tensor | None = None,
+                                       max_capacity_hint: int | None = None, fp32_projection: bool = False,
+                                       risk_safe_observer: bool = False, raw_value: torch.Tensor | None = None,
+                                       value_block_size: int = 64) -> torch.Tensor:
+    """VASC value-risk pair-debt selection of one layer (SW:3632-4098).
+
+    Returns the bool support ``[B,H,Q,K]`` with exactly
+    ``min(base_mask.sum(-1), M)`` blocks per row and updates
+    ``routing_state`` in place. Arithmetic is float32 with the conservative
+    projections of the release configuration (``fp32_projection`` has no
+    further effect there).
+    """
+    if pooled_score.ndim != 4 or base_mask.shape != pooled_score.shape:
+        raise ValueError("CoSA pair debt requires matching [B,H,Q,K] scores")
+    if pooled_value is None and raw_value is None:
+        raise ValueError("CoSA pair debt requires pooled or raw values")
+    if pooled_value is not None and pooled_value.ndim != 4:
+        raise ValueError("CoSA pair debt requires pooled [B,H,K,D] values")
+    if pooled_value is not None and pooled_value.shape[:2] != pooled_score.shape[:2]:
+        raise ValueError("pooled score/value batch and head dimensions differ")
+    if pooled_value is not None and pooled_value.shape[-2] != pooled_score.shape[-1]:
+        raise ValueError("pooled score/value key layouts differ")
+    if raw_value is not None and raw_value.shape[:2] != pooled_score.shape[:2]:
+        raise ValueError("raw value batch and head dimensions differ")
+    if base_mask.dtype != torch.bool:
+        raise ValueError("base_mask must be boolean")
+    if layer_idx < 0:
+        raise ValueError("layer_idx must be non-negative")
+    if routing_state is None:
+        raise ValueError("CoSA pair debt requires routing_state")
+    if protected_mask is not None and protected_mask.shape != base_mask.shape:
+        raise ValueError("protected mask must match the QK support")
+    if max_capacity_hint is not None and max_capacity_hint < 0:
+        raise ValueError("max capacity hint must be non-negative")
+    if risk_safe_observer:
+        raise NotImplementedError("the risk-safe observer is a research diagnostic and is not built")
+    _require_gpu(pooled_score, "pooled_score")
+    B, H, Q, K = pooled_score.shape
+    P = (K + 1) // 2
+    cap = base_mask.sum(-1, dtype=torch.int32)
+    M = min(int(max_capacity_hint), K) if max_capacity_hint is not None else int(cap.max().item()) if cap.numel() else 0
+    if stats_store is not None and bool((cap > M).any()):
+        raise RuntimeError("capacity hint is smaller than the QK budget")
+    if pooled_value is not None:
+        innovation = ops.pair_innovation(pooled_value)
+    else:
+        if value_block_size != KBLK:
+            raise NotImplementedError("value pooling is built for 64-token blocks")
+        _, _, _, innovation = ops.pool_qkv(v=raw_value)
+        if innovation.shape[-1] != P:
+            raise RuntimeError("fused value pooling changed the QK block layout")
+    debt, pending, service = _ledger_inputs(routing_state, B, H, P)
+    out = ops.select_blocks(pooled_score, mode=_lib.MODE_VASC, topk=0, innovation=innovation, row_cap=cap,
+                            protected_mask=protected_mask, max_capacity=M, debt=debt, pending_arrival=pending,
+                            prev_service=service, want_mask=True, want_priority=True)
+    _ledger_outputs(routing_state, out, pooled_score, layer_idx, M)
+    if stats_store is not None:
+        stats_store.update(_stats(out, cap))
+    return out["mask"].bool()
+
+
+def finalize_cosa_value_risk_pair_debt(routing_state: dict | None, *, stats_store: dict | None = None) -> dict:
+    """Settle the last layer's service into the ledger (SW:4101-4177).
+
+    Returns the terminal statistics, or ``{}`` when nothing is pending (so a
+    second call returns ``{}``).
+    """
+    if routing_state is None:
+        return {}
+    pending = routing_state.pop(PENDING_KEY, None)
+    pending_layer = routing_state.pop(PENDING_LAYER_KEY, None)
+    if pending is None:
+        return {}
+    obs = routing_state.pop(SERVICE_KEY, None)
+    if obs is None or not obs.get("identity_observed", False):
+        raise RuntimeError("terminal CoSA settlement requires exact PV service")
+    if obs.get("layer_idx") != pending_layer:
+        raise RuntimeError("terminal PV service does not match CoSA layer")
+    if "pair_service_fraction" not in obs:
+        raise NotImplementedError("only the qk_admission service domain is built")
+    service = obs["pair_service_fraction"]
+    prev = routing_state.get(STATE_KEY)
+    if prev is not None and tuple(prev.shape) != tuple(pending.shape):
+        prev = None
+    terminal = ops.settle_terminal(prev, pending, service).view(pending.shape)
+    routing_state[STATE_KEY] = terminal
+    dev = terminal.device
+    stats = {
+        "cosa_pair_terminal_settled": torch.tensor(1.0, device=dev),
+        "cosa_pair_terminal_layer": torch.tensor(float(pending_layer), device=dev),
+        "cosa_pair_terminal_arrival": pending.sum(dim=-1).mean(),
+        "cosa_pair_terminal_service": service.sum(dim=-1).mean(),
+        "cosa_pair_terminal_backlog": terminal.sum(dim=-1).mean(),
+    }
+    if stats_store is not None:
+        stats_store.update(stats)
+    return stats
+
+
+def _check_research_kwargs(kwargs: dict) -> None:
+    for name, value in kwargs.items():
+        if name in _RESEARCH_DEFAULTS:
+            default = _RESEARCH_DEFAULTS[name]
+            same = value is default or (value == default if not isinstance(value, torch.Tensor) else False)
+            if not same:
+                raise NotImplementedError(f"{name}={value!r} selects a research router that is not built")
+        elif name.startswith(_INERT_WITHOUT_ROUTER):
+            continue
+        else:
+            raise TypeError(f"block_sparse_attn_cuda() got an unexpected keyword argument {name!r}")
+
+
+def block_sparse_attn_cuda(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                           pooled_score: torch.Tensor, topk: int | None = None, sparse_ratio: float | None = None,
+                           cdf_threshold: float | None = None, return_sparsity: bool = False,
+                           dtype: torch.dtype = torch.float16, *, layer_idx: int = 0,
+                           routing_stats_store: dict | None = None, routing_state: dict | None = None,
+                           num_patch_tokens: int | None = None, **research):
+    """Sparse global attention of the patch queries (SW:6868-8245).
+
+    query ``[B,H,Nq,D]`` (patch queries), key/value ``[B,H,Tk,D]`` with the
+    special tokens appended, pooled_score ``[B,H,ceil(Nq/128),ceil(Np/64)]``.
+    The selection mode follows the reference's ``SPARSE_VGGT_*`` switches
+    (``vasc`` when ``COSA_VALUE_RISK_PAIR_DEBT`` is on, else ``topk``).
+    ``dtype`` is accepted for signature compatibility: the kernel computes
+    in bf16. Returns ``o`` (query dtype) or ``(o, sparsity)``.
+    """
+    _check_research_kwargs(research)
+    for t, name in ((query, "query"), (key, "key"), (value, "value"), (pooled_score, "pooled_score")):
+        _require_gpu(t, name)
+    cfg = routing_config()
+    out_dtype = query.dtype
+    Tk = key.shape[-2]
+    orig_kblk = pooled_score.shape[-1]
+    total_kblk = math.ceil(Tk / KBLK)
+    sink = total_kblk - orig_kblk
+    if sink < 0:
+        raise ValueError("pooled_score has more key blocks than the keys")
+    t = _budget(orig_kblk, topk, sparse_ratio, cdf_threshold)
+    mixed = num_patch_tokens is not None and num_patch_tokens < Tk and num_patch_tokens % KBLK != 0
+    force_last = mixed and not cfg.official_mask
+    if cfg.mode == "vasc":
+        if num_patch_tokens is None:
+            raise ValueError("CoSA pair debt requires patch metadata")
+        if routing_state is None:
+            raise ValueError("CoSA pair debt requires routing_state")
+        B, H = pooled_score.shape[:2]
+        P = (orig_kblk + 1) // 2
+        _, _, _, innovation = ops.pool_qkv(v=value[..., :num_patch_tokens, :])
+        hint = (t + int(force_last)) if (sparse_ratio is not None and topk is None) else None
+        if hint is None:
+            hint = max(t, 1) + int(force_last)
+        debt, pending, service = _ledger_inputs(routing_state, B, H, P)
+        sel = ops.select_blocks(pooled_score, mode=_lib.MODE_VASC, topk=t, innovation=innovation,
+                                force_last=force_last, max_capacity=hint, sink_blocks=sink, debt=debt,
+                                pending_arrival=pending, prev_service=service,
+                                want_priority=not cfg.skip_routing_stats)
+        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, min(hint, orig_kblk))
+        if routing_stats_store is not None:
+            routing_stats_store.update(_stats(sel, None))
+    else:
+        sel = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=t, force_last=force_last,
+                                sink_blocks=sink)
+    vt = ops.pack_v(value)
+    o = ops.block_sparse_attn(query, key, vt, sel["index"], sel["count"])
+    if o.dtype != out_dtype:
+        o = o.to(out_dtype)
+    if return_sparsity:
+        kept = sel["count"].sum(dtype=torch.float64)
+        sparsity = (1.0 - kept / float(sel["count"].numel() * total_kblk)).float()
+        return o, sparsity
+    return o
