@@ -30,7 +30,9 @@ COMMON_FLAGS = [
 # every float32 operation separately to stay bit-identical with the oracle.
 SOURCES = {
     "capi.cpp": [],
-    "attn.hip": [],
+    # MFMA accumulators in VGPRs (no AGPR round trips in the softmax loop);
+    # no NaN canonicalisation around the running max.
+    "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
     "pack.hip": [],
     "pool.hip": ["-ffp-contract=off"],
     "select.hip": ["-ffp-contract=off"],

@@ -11,13 +11,21 @@
 //    lane owns one query row (lane % 32) and 32 of the 64 keys: the row max
 //    and row sum are lane-local plus one xor-32 exchange.
 //  * O^T = Vt P^T on the same MFMA, so P feeds the B operand straight from
-//    the S^T accumulators and the rescale by exp2(m_old - m_new) is
-//    lane-local. Vt comes from vasc_pack_v with keys permuted into exactly
-//    the order the accumulators hold them.
-//  * K and Vt tiles are double-buffered in LDS (2 x 16 KB) with an xor
-//    swizzle of the 16-byte chunks (chunk ^ row%8) so every ds_read_b128 of
-//    an MFMA operand is bank-conflict free; the next block's global loads
-//    are in flight during the current block's MFMAs.
+//    the S^T accumulators and the rescale is lane-local. Vt comes from
+//    vasc_pack_v with keys permuted into exactly the order the accumulators
+//    hold them. The row sum is taken on the bf16-rounded P with v_dot2 so the
+//    normaliser matches the P the MFMA consumes.
+//  * Lazy rescaling: the running max only moves (and O is only rescaled)
+//    when a block raises it by more than 8 in log2 units; P then stays below
+//    2^8, far inside bf16 and fp32 range, and the result is unchanged up to
+//    rounding. Most blocks skip the 32 multiplies.
+//  * K and Vt tiles arrive through global_load_lds_dwordx4 straight into a
+//    double-buffered LDS tile (2 x 16 KB), one block ahead of the MFMAs, with
+//    a 16-byte-chunk xor swizzle ((row/2)%8) that spreads the 32 rows an
+//    MFMA operand read touches over all LDS banks.
+//  * Accumulators stay in VGPRs (built with -mllvm -amdgpu-mfma-vgpr-form,
+//    no AGPR copies) and the kernel is held to 128 VGPRs so four waves share
+//    each SIMD: one wave's MFMAs overlap another's exp/VALU work.
 //  * workgroup ids are remapped so each XCD walks a contiguous range of
 //    query blocks of the same head (K/V reuse in that XCD's L2).
 #include "common.h"
@@ -53,8 +61,21 @@ __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Sum of a packed bf16 pair added to acc (v_dot2c_f32_bf16 with (1, 1)).
+__device__ __forceinline__ float add_bf16_pair(uint32_t pair, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
+                                         __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+}
+
+// LDS chunk swizzle of tile row r (16-byte chunks, 8 per 128-byte row).
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
+constexpr float kLazyLog2 = 8.0f;  // rescale only when the max grows by > 2^8
+
 template <bool kDense>
-__global__ __launch_bounds__(kThreads) void bsattn_fwd_kernel(const AttnParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void bsattn_fwd_kernel(const AttnParams p) {
+  constexpr int CH = 512 / kThreads;  // 16-byte chunks per thread per tile
   __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][kTile];
 
   const int64_t wg = xcd_remap(blockIdx.x, p.num_wg);
@@ -97,128 +118,133 @@ __global__ __launch_bounds__(kThreads) void bsattn_fwd_kernel(const AttnParams p
       qf[s] = qvalid ? *reinterpret_cast<const u32x4 *>(qptr + 16 * s + 8 * hf) : u32x4{0, 0, 0, 0};
   }
 
-  // Global -> LDS staging: thread owns LDS chunks tid and tid + 256, i.e.
-  // rows r0 = tid/8 and r0 + 32 at physical chunk tid%8, which holds logical
-  // chunk (tid%8) ^ (row%8) (identical for both rows).
-  const int r0 = tid >> 3;
-  const int lchunk = (tid & 7) ^ (r0 & 7);
-  const uint16_t *kbase = p.k + b * p.k_sb + h * p.k_sh + lchunk * 8;
-  const uint16_t *vbase = p.vt + (bh * p.nkb) * kTile + lchunk * 8;
-
+  // Staging: LDS chunk ci = u*256 + tid lands at byte 16*ci (global_load_lds
+  // writes lane i of a wave at base + 16*i); it holds tile row ci/8, logical
+  // chunk (ci%8) ^ swz(row), so each lane fetches that global chunk.
+  const uint16_t *kbase = p.k + b * p.k_sb + h * p.k_sh;
+  const uint16_t *vbase = p.vt + (bh * p.nkb) * kTile;
+  const int nk32 = static_cast<int>(p.nk);
+  int krow[CH], kcol[CH], voff[CH];
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    const int ci = u * kThreads + tid;
+    const int r = ci >> 3, c = (ci & 7) ^ swz(r);
+    krow[u] = r;
+    kcol[u] = c * 8;
+    voff[u] = r * kHeadDim + c * 8;
+  }
   auto block_at = [&](int j, int64_t prev) -> int64_t {
     if (kDense) return j;
     const int32_t e = list[j];
     return p.delta ? prev + e : static_cast<int64_t>(e);
   };
-  auto fetch = [&](int64_t blk, u32x4 &k0, u32x4 &k1, u32x4 &v0, u32x4 &v1) {
+  auto fetch = [&](int64_t blk, int buf) {
     const bool ok = blk >= 0 && blk < p.nkb;
-    const int64_t sb = ok ? blk : 0;
-    int64_t t0 = sb * kBlockK + r0, t1 = t0 + 32;
-    t0 = t0 < p.nk ? t0 : p.nk - 1;
-    t1 = t1 < p.nk ? t1 : p.nk - 1;
-    k0 = *reinterpret_cast<const u32x4 *>(kbase + t0 * p.k_st);
-    k1 = *reinterpret_cast<const u32x4 *>(kbase + t1 * p.k_st);
-    const uint16_t *vb = vbase + sb * kTile;
-    v0 = *reinterpret_cast<const u32x4 *>(vb + r0 * kHeadDim);
-    v1 = *reinterpret_cast<const u32x4 *>(vb + (r0 + 32) * kHeadDim);
+    const int sb = ok ? static_cast<int>(blk) : 0;
+    const bool full = (sb + 1) * kBlockK <= nk32;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      int t = sb * kBlockK + krow[u];
+      if (!full) t = t < nk32 ? t : nk32 - 1;
+      const uint16_t *ks = kbase + static_cast<int64_t>(t) * p.k_st + kcol[u];
+      const uint16_t *vs = vbase + static_cast<int64_t>(sb) * kTile + voff[u];
+      uint16_t *kd = &smem[buf][0][(u * kThreads + w * 64) * 8];
+      uint16_t *vd = &smem[buf][1][(u * kThreads + w * 64) * 8];
+      __builtin_amdgcn_global_load_lds(ks, (__attribute__((address_space(3))) void *)kd, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vs, (__attribute__((address_space(3))) void *)vd, 16, 0, 0);
+    }
   };
 
   floatx16 oacc[2];
 #pragma unroll
   for (int i = 0; i < 16; ++i) { oacc[0][i] = 0.f; oacc[1][i] = 0.f; }
-  float m = -INFINITY;
+  float m = -INFINITY;  // running max in log2 units (stale by < kLazyLog2)
   float lsum = 0.f;
 
   int64_t blk = block_at(0, 0);
-  u32x4 pk0, pk1, pv0, pv1;
-  fetch(blk, pk0, pk1, pv0, pv1);
-
+  fetch(blk, 0);
   for (int j = 0; j < n; ++j) {
     const int buf = j & 1;
-    uint16_t *ks = smem[buf][0];
-    uint16_t *vs = smem[buf][1];
-    *reinterpret_cast<u32x4 *>(ks + tid * 8) = pk0;
-    *reinterpret_cast<u32x4 *>(ks + (tid + 256) * 8) = pk1;
-    *reinterpret_cast<u32x4 *>(vs + tid * 8) = pv0;
-    *reinterpret_cast<u32x4 *>(vs + (tid + 256) * 8) = pv1;
-    __syncthreads();
-
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // block j landed; every wave is done with buffer buf^1
     const int64_t cur = blk;
     if (j + 1 < n) {
       blk = block_at(j + 1, blk);
-      fetch(blk, pk0, pk1, pv0, pv1);
+      fetch(blk, buf ^ 1);
     }
+    const uint16_t *ks = smem[buf][0];
+    const uint16_t *vs = smem[buf][1];
 
     // S^T tiles: keys 32t + [0,32) x this wave's 32 query rows.
     floatx16 sacc[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int i = 0; i < 16; ++i) sacc[t][i] = 0.f;
-      const int row = 32 * t + lr;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int chunk = (2 * s + hf) ^ (row & 7);
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(ks + row * kHeadDim + chunk * 8);
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int row = 32 * t + lr;
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(ks + row * kHeadDim + ((2 * s + hf) ^ swz(row)) * 8);
         sacc[t] = mfma32(a, qf[s], sacc[t]);
       }
-    }
 
     // Mask keys past the sequence end and blocks outside [0, nkb).
     const bool blk_ok = cur >= 0 && cur < p.nkb;
-    if (!blk_ok || (cur + 1) * kBlockK > p.nk) {
-      const int64_t base = cur * kBlockK;
+    const int lim = blk_ok ? nk32 - static_cast<int>(cur) * kBlockK : 0;
+    if (__builtin_expect(lim < kBlockK, 0)) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kk = 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
-          if (!blk_ok || base + kk >= p.nk) sacc[t][r] = -INFINITY;
+          sacc[t][r] = kk < lim ? sacc[t][r] : -INFINITY;
         }
     }
 
-    float mx = sacc[0][0];
+    float mx = fmaxf(sacc[0][0], sacc[0][1]);
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[0][r]);
+    for (int r = 2; r < 16; ++r) mx = fmaxf(mx, sacc[0][r]);
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[1][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m, mx * p.c);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-    m = m_new;
-
-    float psum = 0.f;
+    const bool grow = m_new > m + kLazyLog2;
+    if (__ballot(grow)) {
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], p.c, -m_use));
-        sacc[t][r] = e;
-        psum += e;
-      }
-    lsum = lsum * alpha + psum;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
+      for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
+      lsum *= alpha;
+      m = grow ? m_new : m;
+    }
+    const float m_use = m == -INFINITY ? 0.f : m;
 
     // P^T as B operand: step s uses accumulators 8(s%2)..+7 of tile s/2.
     u32x4 pb[4];
+    float ls = lsum;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int t = s >> 1, r = 8 * (s & 1);
-      pb[s] = u32x4{pack_bf16x2(sacc[t][r + 0], sacc[t][r + 1]), pack_bf16x2(sacc[t][r + 2], sacc[t][r + 3]),
-                    pack_bf16x2(sacc[t][r + 4], sacc[t][r + 5]), pack_bf16x2(sacc[t][r + 6], sacc[t][r + 7])};
+      uint32_t d[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = __builtin_amdgcn_exp2f(fmaf(sacc[t][r + 2 * e], p.c, -m_use));
+        const float x1 = __builtin_amdgcn_exp2f(fmaf(sacc[t][r + 2 * e + 1], p.c, -m_use));
+        d[e] = pack_bf16x2(x0, x1);
+        ls = add_bf16_pair(d[e], ls);
+      }
+      pb[s] = u32x4{d[0], d[1], d[2], d[3]};
     }
+    lsum = ls;
 #pragma unroll
-    for (int n2 = 0; n2 < 2; ++n2) {
-      const int row = 32 * n2 + lr;
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int chunk = (2 * s + hf) ^ (row & 7);
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(vs + row * kHeadDim + chunk * 8);
+      for (int n2 = 0; n2 < 2; ++n2) {
+        const int row = 32 * n2 + lr;
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(vs + row * kHeadDim + ((2 * s + hf) ^ swz(row)) * 8);
         oacc[n2] = mfma32(a, pb[s], oacc[n2]);
       }
-    }
   }
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
