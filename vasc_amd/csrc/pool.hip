@@ -43,10 +43,22 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int dc = tid & 7, r = tid >> 3;
 
+  // Issue all 12 row loads (3 tensors x 4 rows) before any reduction so each
+  // thread keeps 192 bytes in flight.
+  u32x4 raw[3][4];
+#pragma unroll
+  for (int X = 0; X < 3; ++X) {
+    const uint16_t *src = p.x[X] ? p.x[X] + b * p.sb[X] + h * p.sh[X] + dc * 8 : nullptr;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t tok = chunk * 128 + r + 32 * u;
+      raw[X][u] = (src && tok < p.ntok[X]) ? *reinterpret_cast<const u32x4 *>(src + tok * p.st[X])
+                                           : u32x4{0, 0, 0, 0};
+    }
+  }
 #pragma unroll
   for (int X = 0; X < 3; ++X) {
     if (p.x[X] == nullptr) continue;
-    const uint16_t *src = p.x[X] + b * p.sb[X] + h * p.sh[X] + dc * 8;
     float acc[2][8];
 #pragma unroll
     for (int half = 0; half < 2; ++half)
@@ -54,14 +66,10 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
       for (int i = 0; i < 8; ++i) acc[half][i] = 0.f;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int64_t tok = chunk * 128 + r + 32 * u;
-      if (tok < p.ntok[X]) {
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(src + tok * p.st[X]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[u >> 1][2 * i] += __uint_as_float(v[i] << 16);
-          acc[u >> 1][2 * i + 1] += __uint_as_float(v[i] & 0xffff0000u);
-        }
+      for (int i = 0; i < 4; ++i) {
+        acc[u >> 1][2 * i] += __uint_as_float(raw[X][u][i] << 16);
+        acc[u >> 1][2 * i + 1] += __uint_as_float(raw[X][u][i] & 0xffff0000u);
       }
     }
 #pragma unroll
@@ -163,12 +171,14 @@ __device__ __forceinline__ floatx16 pooled_tile(const uint16_t *pk, int64_t kb, 
   return acc;
 }
 
-__global__ __launch_bounds__(256) void pooled_softmax_kernel(const uint16_t *__restrict__ pq,
-                                                             const uint16_t *__restrict__ pk, int64_t qb,
-                                                             int64_t kb, float scale, int round,
-                                                             float *__restrict__ prob) {
-  __shared__ float sm_m[4][32];
-  __shared__ float sm_s[4][32];
+constexpr int kSoftmaxWaves = 16;  // key tiles of one 32-row strip spread over 16 waves
+
+__global__ __launch_bounds__(kSoftmaxWaves * 64) void pooled_softmax_kernel(const uint16_t *__restrict__ pq,
+                                                                           const uint16_t *__restrict__ pk,
+                                                                           int64_t qb, int64_t kb, float scale,
+                                                                           int round, float *__restrict__ prob) {
+  __shared__ float sm_m[kSoftmaxWaves][32];
+  __shared__ float sm_s[kSoftmaxWaves][32];
   const int64_t bh = blockIdx.y;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 32;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 31, hf = l >> 5;
@@ -183,7 +193,7 @@ __global__ __launch_bounds__(256) void pooled_softmax_kernel(const uint16_t *__r
   const int64_t ntiles = cdiv(kb, 32);
 
   float m = -INFINITY, sum = 0.f;
-  for (int64_t t = w; t < ntiles; t += 4) {
+  for (int64_t t = w; t < ntiles; t += kSoftmaxWaves) {
     const floatx16 x = pooled_tile(kbase, kb, t, qf, lr, hf, scale, round != 0);
     float mx = x[0];
 #pragma unroll
@@ -209,17 +219,17 @@ __global__ __launch_bounds__(256) void pooled_softmax_kernel(const uint16_t *__r
   __syncthreads();
   float gm = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) gm = fmaxf(gm, sm_m[i][lr]);
+  for (int i = 0; i < kSoftmaxWaves; ++i) gm = fmaxf(gm, sm_m[i][lr]);
   float gs = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kSoftmaxWaves; ++i) {
     const float mi = sm_m[i][lr];
     if (mi != -INFINITY) gs += sm_s[i][lr] * expf(mi - gm);
   }
   const float inv = 1.f / gs;
   // Lanes of padding rows stay: they feed key rows to the MFMA A operand.
   float *out = prob + (bh * qb + (qok ? qrow : 0)) * kb;
-  for (int64_t t = w; t < ntiles; t += 4) {
+  for (int64_t t = w; t < ntiles; t += kSoftmaxWaves) {
     const floatx16 x = pooled_tile(kbase, kb, t, qf, lr, hf, scale, round != 0);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -302,7 +312,7 @@ extern "C" int vasc_pooled_softmax(const uint16_t *pooled_q, const uint16_t *poo
   VASC_REQUIRE((reinterpret_cast<uintptr_t>(pooled_q) & 15) == 0 && (reinterpret_cast<uintptr_t>(pooled_k) & 15) == 0,
                "pooled inputs must be 16-byte aligned");
   VASC_REQUIRE(B * H < 65536, "grid too large");
-  hipLaunchKernelGGL(pooled_softmax_kernel, dim3(cdiv(qb, 32), B * H), dim3(256), 0,
+  hipLaunchKernelGGL(pooled_softmax_kernel, dim3(cdiv(qb, 32), B * H), dim3(kSoftmaxWaves * 64), 0,
                      reinterpret_cast<hipStream_t>(stream), pooled_q, pooled_k, qb, kb, scale, round_bf16, prob);
   return check_launch("vasc_pooled_softmax");
 }

@@ -18,11 +18,12 @@
 //   global    wave sum per head, then a seq sum over heads (the gate).
 // Selection keeps the c largest priorities, ties to the lower block index.
 //
-// Launches (VASC mode): settle (one wave per head) -> arrival (one wave per
-// row) -> colsum (one thread per pair column and 32-row chunk) -> head (one
-// thread per pair column) -> select (one wave per row, radix select on
-// order-preserving uint32 keys staged in LDS) -> service. Top-K mode runs the
-// select launch alone. Every launch is short and wide: no long serial chains.
+// Launches (VASC mode): arrival (one wave per row) -> colsum (one thread per
+// pair column and 32-row chunk) -> head (ledger settlement, arrival mean,
+// admitted debt; one thread per pair column) -> select (one wave per row,
+// radix select on order-preserving uint32 keys staged in LDS) -> service.
+// Top-K mode runs the select launch alone. Every launch is short and wide:
+// no long serial chains.
 #pragma clang fp contract(off)
 
 #include "common.h"
@@ -32,7 +33,7 @@ namespace {
 
 constexpr float kFltMax = 3.402823466e38f;
 constexpr float kFltMin = 1.175494351e-38f;
-constexpr int kRowsPerWg = 16;  // select: 4 waves x 4 rows of one head
+constexpr int kRowsPerWg = 4;   // select: one row per wave, 4 rows of one head
 constexpr int kChunk = 32;      // rows per partial of the arrival mean
 
 __device__ __forceinline__ uint32_t order_key(float x) {
@@ -72,45 +73,25 @@ struct SelectParams {
   int64_t width;
   int32_t *count_out;
   // workspace
-  float *total, *rowpair, *a, *adm, *dsum;
+  float *total, *rowpair, *a, *adm;
   double *part, *gate_part;
   int32_t *cap, *counts;
   int64_t nchunks;
 };
 
 // ------------------------------------------------------------------ settle
-// One wave per head: settled debt, its sum, and the head's partials of the
-// three global gate sums (useful repayment, reflection, service).
-__global__ __launch_bounds__(64) void settle_kernel(const SelectParams p) {
-  const int64_t bh = blockIdx.x;
-  const int lane = threadIdx.x;
-  double dacc = 0.0, useful = 0.0, wasted = 0.0, consumed = 0.0;
-  for (int64_t pp = lane; pp < p.P; pp += 64) {
-    const int64_t i = bh * p.P + pp;
-    const float d0 = p.debt_in ? clamp_min0(p.debt_in[i]) : 0.f;
-    float d = d0;
-    if (p.pending) {
-      const float sig = p.prev_service ? p.prev_service[i] : 0.f;
-      const float u = (d0 + p.pending[i]) - sig;
-      const float refl = clamp_min0(-u);
-      d = clamp_min0(u);
-      useful = useful + static_cast<double>(clamp_min0(sig - refl));
-      wasted = wasted + static_cast<double>(refl);
-      consumed = consumed + static_cast<double>(sig);
-    }
-    p.debt_out[i] = d;
-    dacc = dacc + static_cast<double>(d);
+// Settled debt of one ledger entry (sparse_wrapper.py:3793-3832).
+__device__ __forceinline__ float settle_one(const SelectParams &p, int64_t i, float *refl, float *sig) {
+  const float d0 = p.debt_in ? clamp_min0(p.debt_in[i]) : 0.f;
+  if (!p.pending) {
+    *refl = 0.f;
+    *sig = 0.f;
+    return d0;
   }
-  dacc = wave_butterfly(dacc);
-  useful = wave_butterfly(useful);
-  wasted = wave_butterfly(wasted);
-  consumed = wave_butterfly(consumed);
-  if (lane == 0) {
-    p.dsum[bh] = static_cast<float>(dacc);
-    p.gate_part[3 * bh + 0] = useful;
-    p.gate_part[3 * bh + 1] = wasted;
-    p.gate_part[3 * bh + 2] = consumed;
-  }
+  *sig = p.prev_service ? p.prev_service[i] : 0.f;
+  const float u = (d0 + p.pending[i]) - *sig;
+  *refl = clamp_min0(-u);
+  return clamp_min0(u);
 }
 
 // Global service gate (sparse_wrapper.py:3837-3842) from the per-head
@@ -199,16 +180,39 @@ __global__ __launch_bounds__(256) void colsum_kernel(const SelectParams p) {
   p.part[(bh * p.nchunks + chunk) * p.P + pp] = acc;
 }
 
-// Pending arrival (mean over rows), pair capacity and admitted debt.
+// Per head: ledger settlement, pending arrival (mean over rows), pair
+// capacity and admitted debt. Wave 0 of every workgroup recomputes the head's
+// debt sum and pair capacity (canonical wave sums); workgroup 0 of the head
+// also publishes the head's partials of the three global gate sums.
 __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
-  __shared__ float sh_pc;
+  __shared__ float sh_pc, sh_dsum;
   const int64_t bh = blockIdx.y;
   const int tid = threadIdx.x;
   if (tid < 64) {
-    double acc = 0.0;
+    double acc = 0.0, dacc = 0.0, useful = 0.0, wasted = 0.0, consumed = 0.0;
     for (int64_t q = tid; q < p.Q; q += 64) acc = acc + static_cast<double>(p.rowpair[bh * p.Q + q]);
+    for (int64_t pp = tid; pp < p.P; pp += 64) {
+      float refl, sig;
+      const float d = settle_one(p, bh * p.P + pp, &refl, &sig);
+      dacc = dacc + static_cast<double>(d);
+      useful = useful + static_cast<double>(clamp_min0(sig - refl));
+      wasted = wasted + static_cast<double>(refl);
+      consumed = consumed + static_cast<double>(sig);
+    }
     const double s = wave_butterfly(acc);
-    if (tid == 0) sh_pc = static_cast<float>(s / static_cast<double>(p.Q));
+    const double ds = wave_butterfly(dacc);
+    useful = wave_butterfly(useful);
+    wasted = wave_butterfly(wasted);
+    consumed = wave_butterfly(consumed);
+    if (tid == 0) {
+      sh_pc = static_cast<float>(s / static_cast<double>(p.Q));
+      sh_dsum = static_cast<float>(ds);
+      if (blockIdx.x == 0) {
+        p.gate_part[3 * bh + 0] = useful;
+        p.gate_part[3 * bh + 1] = wasted;
+        p.gate_part[3 * bh + 2] = consumed;
+      }
+    }
   }
   __syncthreads();
   const int64_t pp = static_cast<int64_t>(blockIdx.x) * 256 + tid;
@@ -219,9 +223,11 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
   for (int64_t c = 0; c < p.nchunks; ++c) acc = acc + part[c * p.P];
   p.arrival_out[bh * p.P + pp] = static_cast<float>(acc / static_cast<double>(p.Q));
   p.counts[bh * p.P + pp] = 0;
-  const float dsum = p.dsum[bh];
+  float refl, sig;
+  const float d = settle_one(p, bh * p.P + pp, &refl, &sig);
+  p.debt_out[bh * p.P + pp] = d;
+  const float dsum = sh_dsum;
   const float scale = sh_pc / floor_tiny(dsum);
-  const float d = p.debt_out[bh * p.P + pp];
   p.adm[bh * p.P + pp] = dsum > 0.f ? clamp01(d * scale) : 0.f;
 }
 
@@ -381,7 +387,7 @@ __global__ void settle_terminal_kernel(const float *debt_in, const float *pendin
 }
 
 struct Workspace {
-  size_t total, rowpair, cap, a, adm, dsum, part, gate_part, counts, bytes;
+  size_t total, rowpair, cap, a, adm, part, gate_part, counts, bytes;
 };
 
 Workspace layout(int64_t B, int64_t H, int64_t Q, int64_t K) {
@@ -393,7 +399,6 @@ Workspace layout(int64_t B, int64_t H, int64_t Q, int64_t K) {
   w.cap = off;     off += align256(BH * Q * 4);
   w.a = off;       off += align256(BH * Q * P * 4);
   w.adm = off;     off += align256(BH * P * 4);
-  w.dsum = off;    off += align256(BH * 4);
   w.part = off;    off += align256(BH * static_cast<size_t>(cdiv(Q, kChunk)) * P * 8);
   w.gate_part = off; off += align256(BH * 3 * 8);
   w.counts = off;  off += align256(BH * P * 4);
@@ -475,7 +480,6 @@ extern "C" int vasc_select_blocks(const float *score, const float *innovation, i
   p.cap = vasc ? reinterpret_cast<int32_t *>(wsb + ws.cap) : nullptr;
   p.a = vasc ? reinterpret_cast<float *>(wsb + ws.a) : nullptr;
   p.adm = vasc ? reinterpret_cast<float *>(wsb + ws.adm) : nullptr;
-  p.dsum = vasc ? reinterpret_cast<float *>(wsb + ws.dsum) : nullptr;
   p.part = vasc ? reinterpret_cast<double *>(wsb + ws.part) : nullptr;
   p.gate_part = vasc ? reinterpret_cast<double *>(wsb + ws.gate_part) : nullptr;
   p.nchunks = cdiv(Q, kChunk);
@@ -487,8 +491,6 @@ extern "C" int vasc_select_blocks(const float *score, const float *innovation, i
   VASC_SUPPORTED(lds <= 160 * 1024, "select needs %zu bytes of LDS", lds);
   int rc;
   if (vasc) {
-    hipLaunchKernelGGL(settle_kernel, dim3(p.BH), dim3(64), 0, s, p);
-    if ((rc = check_launch("vasc_select_blocks/settle"))) return rc;
     hipLaunchKernelGGL(arrival_kernel, dim3(cdiv(rows, 4)), dim3(256), 0, s, p);
     if ((rc = check_launch("vasc_select_blocks/arrival"))) return rc;
     hipLaunchKernelGGL(colsum_kernel, dim3(cdiv(p.P, 256), p.nchunks, p.BH), dim3(256), 0, s, p);
