@@ -31,6 +31,23 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 
 
+TRAFFIC_SUMMARY = "profiles/traffic_c2_step.md"
+
+
+def traffic_bytes():
+    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary of this workload (calibrated against a plain copy)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_SUMMARY)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("attention_traffic_bytes_per_launch:"):
+                    return float(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -108,6 +125,21 @@ def run_step(layers, ratios, ledger, timer, keep=None):
             keep.append((sel["index"], sel["count"], o))
 
 
+def attention_min_bytes(index, count, n_q, n_k, d):
+    """Least HBM bytes one sparse-attention launch can move: Q read and O written
+    once, plus every K block and packed V tile that some query block of the
+    head selects, each read once (bf16)."""
+    kb = -(-n_k // 64)
+    width = index.shape[-1]
+    valid = torch.arange(width, device=index.device) < count.unsqueeze(-1).long()
+    idx = torch.where(valid, index.long(), kb).flatten(2)
+    touched = torch.zeros(*idx.shape[:2], kb + 1, dtype=torch.bool, device=idx.device)
+    touched.scatter_(2, idx, True)
+    blocks = int(touched[..., :kb].sum().item())
+    heads = index.shape[0] * index.shape[1]
+    return heads * n_q * d * 2 * 2 + blocks * 64 * d * 2 * 2
+
+
 def cpu_baseline(layer, ratio, frames, n_layers):
     from oracle import cpu_baseline as cb
     cores = len(os.sched_getaffinity(0))
@@ -141,6 +173,8 @@ def main() -> int:
     ap.add_argument("--graph", dest="graph", action="store_true", default=True,
                     help="replay the step as a HIP graph (default)")
     ap.add_argument("--no-graph", dest="graph", action="store_false")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="untimed: a 256 MiB copy (counter calibration) then one eager step, for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -160,6 +194,15 @@ def main() -> int:
     layers = [synthetic_layer(N, P, S, H, D, seed=li, device=dev) for li in range(L)]
     torch.cuda.synchronize()
     ledger = pipeline.Ledger()
+
+    if args.traffic_probe:
+        src = torch.empty(128 * 2**20, dtype=torch.bfloat16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # 256 MiB read + 256 MiB written: the FETCH_SIZE / WRITE_SIZE scale
+        run_step(layers, ratios, ledger, Timer(enabled=False))
+        torch.cuda.synchronize()
+        log("traffic probe done")
+        return 0
 
     log(f"warmup {args.warmup} steps")
     for _ in range(args.warmup):
@@ -187,6 +230,7 @@ def main() -> int:
     run_step(layers, ratios, ledger, Timer(enabled=False), keep)
     n_patch, n_total = N * (P - S), N * P
     attn_flops_step = sum(pipeline.attention_flops((i, c), n_patch, n_total, D) for i, c, _ in keep)
+    attn_min_bytes_step = sum(attention_min_bytes(i, c, n_patch, n_total, D) for i, c, _ in keep)
     eager_out = [o.clone() for _, _, o in keep]
     eager_lists = [(i.clone(), c.clone()) for i, c, _ in keep]
     del keep
@@ -261,8 +305,10 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": traffic_bytes(),
+            "traffic_source": TRAFFIC_SUMMARY,
             "flops_per_launch": attn_flops_step / L,
+            "min_hbm_bytes_per_launch": attn_min_bytes_step / L,
             "ms_per_launch": attn_ms_launch,
         },
     }

@@ -84,7 +84,8 @@ void bsattn_fwd_kernel(const AttnParams p) {
   const int64_t h = bh % p.H;
   const int64_t b = bh / p.H;
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, lr = l & 31, hf = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
+  const int l = tid & 63, lr = l & 31, hf = l >> 5;
 
   int n;
   const int32_t *list = nullptr;
@@ -124,34 +125,41 @@ void bsattn_fwd_kernel(const AttnParams p) {
   const uint16_t *kbase = p.k + b * p.k_sb + h * p.k_sh;
   const uint16_t *vbase = p.vt + (bh * p.nkb) * kTile;
   const int nk32 = static_cast<int>(p.nk);
-  int krow[CH], kcol[CH], voff[CH];
+  const int nkb32 = static_cast<int>(p.nkb);
+  int64_t koff[CH];
+  int krow[CH], voff[CH];
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
     const int ci = u * kThreads + tid;
     const int r = ci >> 3, c = (ci & 7) ^ swz(r);
     krow[u] = r;
-    kcol[u] = c * 8;
+    koff[u] = static_cast<int64_t>(r) * p.k_st + c * 8;
     voff[u] = r * kHeadDim + c * 8;
   }
-  auto block_at = [&](int j, int64_t prev) -> int64_t {
+  auto block_at = [&](int j, int prev) -> int {
     if (kDense) return j;
     const int32_t e = list[j];
-    return p.delta ? prev + e : static_cast<int64_t>(e);
+    return p.delta ? prev + e : e;
   };
-  auto fetch = [&](int64_t blk, int buf) {
-    const bool ok = blk >= 0 && blk < p.nkb;
-    const int sb = ok ? static_cast<int>(blk) : 0;
+  // Issue the loads of block blk into LDS buffer buf. Full blocks take the
+  // precomputed per-thread offsets from a scalar block base; the partial last
+  // block clamps its rows to the sequence end (their scores are masked).
+  auto fetch = [&](int blk, int buf) {
+    const int sb = (blk >= 0 && blk < nkb32) ? blk : 0;
+    const uint16_t *kb = kbase + static_cast<int64_t>(sb) * kBlockK * p.k_st;
+    const uint16_t *vb = vbase + static_cast<int64_t>(sb) * kTile;
     const bool full = (sb + 1) * kBlockK <= nk32;
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-      int t = sb * kBlockK + krow[u];
-      if (!full) t = t < nk32 ? t : nk32 - 1;
-      const uint16_t *ks = kbase + static_cast<int64_t>(t) * p.k_st + kcol[u];
-      const uint16_t *vs = vbase + static_cast<int64_t>(sb) * kTile + voff[u];
+      const uint16_t *ks = kb + koff[u];
+      if (!full) {
+        const int t = sb * kBlockK + krow[u];
+        if (t >= nk32) ks = kbase + static_cast<int64_t>(nk32 - 1) * p.k_st + (koff[u] - static_cast<int64_t>(krow[u]) * p.k_st);
+      }
       uint16_t *kd = &smem[buf][0][(u * kThreads + w * 64) * 8];
       uint16_t *vd = &smem[buf][1][(u * kThreads + w * 64) * 8];
       __builtin_amdgcn_global_load_lds(ks, (__attribute__((address_space(3))) void *)kd, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vs, (__attribute__((address_space(3))) void *)vd, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vb + voff[u], (__attribute__((address_space(3))) void *)vd, 16, 0, 0);
     }
   };
 
@@ -161,13 +169,13 @@ void bsattn_fwd_kernel(const AttnParams p) {
   float m = -INFINITY;  // running max in log2 units (stale by < kLazyLog2)
   float lsum = 0.f;
 
-  int64_t blk = block_at(0, 0);
+  int blk = block_at(0, 0);
   fetch(blk, 0);
   for (int j = 0; j < n; ++j) {
     const int buf = j & 1;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // block j landed; every wave is done with buffer buf^1
-    const int64_t cur = blk;
+    const int cur = blk;
     if (j + 1 < n) {
       blk = block_at(j + 1, blk);
       fetch(blk, buf ^ 1);
@@ -191,8 +199,8 @@ void bsattn_fwd_kernel(const AttnParams p) {
       }
 
     // Mask keys past the sequence end and blocks outside [0, nkb).
-    const bool blk_ok = cur >= 0 && cur < p.nkb;
-    const int lim = blk_ok ? nk32 - static_cast<int>(cur) * kBlockK : 0;
+    const bool blk_ok = cur >= 0 && cur < nkb32;
+    const int lim = blk_ok ? nk32 - cur * kBlockK : 0;
     if (__builtin_expect(lim < kBlockK, 0)) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -301,6 +309,8 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
   p.c = sm_scale * 1.4426950408889634f;
   p.num_wg = B * H * p.nqb;
   VASC_REQUIRE(p.num_wg < (int64_t(1) << 31), "grid too large");
+  VASC_SUPPORTED(nk < (int64_t(1) << 30) && nq < (int64_t(1) << 40), "sequence of %lld keys not built (< 2^30)",
+                 (long long)nk);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (dense)
     hipLaunchKernelGGL(bsattn_fwd_kernel<true>, dim3(p.num_wg), dim3(kThreads), 0, s, p);
