@@ -140,6 +140,110 @@ def attention_min_bytes(index, count, n_q, n_k, d):
     return heads * n_q * d * 2 * 2 + blocks * 64 * d * 2 * 2
 
 
+def hbm_bytes_per_launch(H, n_patch, n_total, d, listed_per_layer):
+    """Algorithmic HBM bytes of one launch of each HBM-bound kernel (B = 1):
+    every input read once and every output written once."""
+    qb, kb = -(-n_patch // 128), -(-n_patch // 64)
+    kbt = -(-n_total // 64)
+    pooled = H * (qb + 2 * kb) * d * 2 + H * (-(-kb // 2)) * 4
+    return {
+        "pool": 3 * H * n_patch * d * 2 + pooled,
+        "pooled_softmax": H * (qb + kb) * d * 2 + H * qb * kb * 4,
+        "select": H * qb * kb * 4 + listed_per_layer * 4 + H * qb * 4,
+        "pack_v": H * n_total * d * 2 + H * kbt * 64 * d * 2,
+    }
+
+
+def median_ms(fn, reps: int, rounds: int = 5) -> float:
+    """Median over rounds of the mean time of ``reps`` back-to-back calls (hipEvents)."""
+    times = []
+    for _ in range(rounds):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) / reps)
+    return statistics.median(times)
+
+
+def c5_lists(T: int, H: int, rho: float, seed: int, device):
+    """The C5 block lists: per query-block row k ~ Poisson(rho*Kb) clipped to
+    [n_forced, Kb]; forced = key blocks holding tokens f*1041 + j (j < 5) of
+    every frame f; the rest drawn uniformly without replacement; ascending."""
+    qb, kb = T // 128, T // 64
+    g = torch.Generator(device=device).manual_seed(seed)
+    frames = -(-T // 1041)
+    tok = (torch.arange(frames, device=device).view(-1, 1) * 1041 + torch.arange(5, device=device)).flatten()
+    forced = torch.unique(tok[tok < T] // 64)
+    nf = forced.numel()
+    lam = torch.full((H, qb), rho * kb, device=device)
+    k = torch.poisson(lam, generator=g).long().clamp(nf, kb)
+    keys = torch.rand(H, qb, kb, device=device, generator=g)
+    keys[:, :, forced] = -1.0  # forced blocks sort first
+    order = torch.argsort(keys, dim=-1)
+    pos = torch.arange(kb, device=device).view(1, 1, kb)
+    chosen = torch.where(pos < k.unsqueeze(-1), order, kb)
+    index = torch.sort(chosen, dim=-1).values.to(torch.int32).unsqueeze(0)
+    del keys, order, chosen
+    return index, k.to(torch.int32).unsqueeze(0)
+
+
+def run_c5(dev) -> int:
+    """C5: each kernel on randn bf16 [1,16,T,64] inputs, T in {16k, 64k, 256k};
+    attention at densities 0.1 / 0.25 / 0.5 of Poisson block lists."""
+    from vasc_amd import _lib, ops, pipeline
+    H, D = 16, 64
+    for T in (16384, 65536, 262144):
+        g = torch.Generator(device=dev).manual_seed(T)
+        q, k, v = (torch.randn(1, H, T, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+        qb, kb = T // 128, T // 64
+        pq, pk, _, iota = ops.pool_qkv(q, k, v)
+        prob = ops.pooled_softmax(pq, pk)
+        topk = int(kb * 0.25)
+        lines = []
+        hbm = hbm_bytes_per_launch(H, T, T, D, 0)
+        t = median_ms(lambda: ops.pool_qkv(q, k, v), 5)
+        lines.append(("pool", t, hbm["pool"], None))
+        t = median_ms(lambda: ops.pooled_softmax(pq, pk), 5)
+        lines.append(("pooled_softmax", t, hbm["pooled_softmax"], None))
+        for mode, name in ((_lib.MODE_TOPK, "select_topk"), (_lib.MODE_VASC, "select_vasc")):
+            kw = dict(mode=mode, topk=topk)
+            if mode == _lib.MODE_VASC:
+                kw.update(innovation=iota, max_capacity=topk, workspace=ops.select_workspace(1, H, qb, kb, dev))
+            sel = ops.select_blocks(prob, **kw)
+            listed = int(sel["count"].sum().item())
+            t = median_ms(lambda: ops.select_blocks(prob, **kw), 5)
+            lines.append((name, t, H * qb * kb * 4 + listed * 4 + H * qb * 4, f"cap {topk} of {kb}"))
+        t = median_ms(lambda: ops.pack_v(v), 5)
+        lines.append(("pack_v", t, hbm["pack_v"], None))
+        for name, t, nbytes, note in lines:
+            rec = {"workload": "C5", "kernel": name, "T": T, "ms": t, "bytes": nbytes,
+                   "GB_s": nbytes / (t * 1e-3) / 1e9, "frac_of_hbm_peak": nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBS}
+            if note:
+                rec["note"] = note
+            print(json.dumps(rec), flush=True)
+        vt = ops.pack_v(v)
+        for rho in (0.1, 0.25, 0.5):
+            index, count = c5_lists(T, H, rho, seed=int(rho * 100) + T, device=dev)
+            flops = pipeline.attention_flops((index, count), T, T, D)
+            t = median_ms(lambda: ops.block_sparse_attn(q, k, vt, index, count), 3 if T > 65536 else 10)
+            print(json.dumps({"workload": "C5", "kernel": "block_sparse_attn", "T": T, "density": rho,
+                              "mean_blocks_per_row": float(count.float().mean().item()), "ms": t,
+                              "flops": flops, "TFLOP_s": flops / (t * 1e-3) / 1e12,
+                              "frac_of_mfma_peak": flops / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}), flush=True)
+            del index, count
+        t = median_ms(lambda: ops.dense_attn(q, k, vt), 1 if T > 65536 else 3, rounds=3)
+        flops = 4.0 * D * H * T * T
+        print(json.dumps({"workload": "C5", "kernel": "dense_attn", "T": T, "ms": t, "flops": flops,
+                          "TFLOP_s": flops / (t * 1e-3) / 1e12,
+                          "frac_of_mfma_peak": flops / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}), flush=True)
+        del q, k, v, vt, prob, pq, pk, iota
+        torch.cuda.empty_cache()
+    return 0
+
+
 def cpu_baseline(layer, ratio, frames, n_layers):
     from oracle import cpu_baseline as cb
     cores = len(os.sched_getaffinity(0))
@@ -166,8 +270,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--frames", type=int, default=32)
-    ap.add_argument("--sparsity", type=float, default=0.75)
+    ap.add_argument("--workload", choices=("c2", "c3", "c5"), default="c2",
+                    help="c2: the metric's configuration (default); c3: 128 frames at s=0.875; "
+                         "c5: per-kernel microbenchmarks at T = 16k/64k/256k (one JSON line per case)")
+    ap.add_argument("--frames", type=int, default=None)
+    ap.add_argument("--sparsity", type=float, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--graph", dest="graph", action="store_true", default=True,
@@ -188,6 +295,13 @@ def main() -> int:
     from vasc_amd.launcher import layer_sparsity
 
     dev = torch.device("cuda:0")
+    if args.workload == "c5":
+        return run_c5(dev)
+    defaults = {"c2": (32, 0.75), "c3": (128, 0.875)}[args.workload]
+    args.frames = defaults[0] if args.frames is None else args.frames
+    args.sparsity = defaults[1] if args.sparsity is None else args.sparsity
+    if args.workload == "c3":
+        args.no_cpu_baseline = True  # the CPU port needs minutes per C3 layer
     N, P, S, H, D, L = args.frames, 1041, 5, 16, 64, 24
     ratios = layer_sparsity("vggt", args.sparsity, "paper") or [args.sparsity] * L
     log(f"generating {L} layers of synthetic Q/K/V ({N} frames x {P} tokens, H={H})")
@@ -231,6 +345,8 @@ def main() -> int:
     n_patch, n_total = N * (P - S), N * P
     attn_flops_step = sum(pipeline.attention_flops((i, c), n_patch, n_total, D) for i, c, _ in keep)
     attn_min_bytes_step = sum(attention_min_bytes(i, c, n_patch, n_total, D) for i, c, _ in keep)
+    listed_step = sum(int(c.sum().item()) for _, c, _ in keep)
+    kernel_bytes = hbm_bytes_per_launch(H, n_patch, n_total, D, listed_step / L)
     eager_out = [o.clone() for _, _, o in keep]
     eager_lists = [(i.clone(), c.clone()) for i, c, _ in keep]
     del keep
@@ -273,7 +389,8 @@ def main() -> int:
         f"attention {attn_ms_launch:.3f} ms/layer, {achieved:.1f} TFLOP/s")
 
     result = {
-        "metric": METRIC,
+        "metric": METRIC if args.workload == "c2" else
+        f"sparse global-attn layer ms + eff. TFLOP/s @{args.sparsity:g} sparsity, {N} frames; frames/s",
         "value": N / (ms_per_step * 1e-3),
         "unit": "frames/s",
         "n_gpus": 1,
@@ -286,8 +403,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1) + per-frame rank-8 (scale 0.5) Q/K/V at the C2 global-layer shape",
         "config": {
-            "workload": "C2 VGGT-shaped global attention: 24 layers x sparse op (pool+softmax, vasc select "
-                        "+ ledger, V pack, block-sparse attention)",
+            "workload": f"{args.workload.upper()} VGGT-shaped global attention: 24 layers x sparse op "
+                        "(pool+softmax, vasc select + ledger, V pack, block-sparse attention)",
             "frames": N, "tokens": n_total, "patch_tokens": n_patch, "heads": H, "head_dim": D,
             "layers": L, "mode": "vasc", "sparsity": args.sparsity, "structural_allocation": True,
         },
@@ -298,6 +415,12 @@ def main() -> int:
         "attn_tflops": achieved,
         "eff_tflops": dense_flops_layer / (layer_ms * 1e-3) / 1e12,
         "kernel_ms_per_step": kernel_ms,
+        "kernels_hbm": {
+            name: {"ms_per_launch": kernel_ms[name] / launches[name], "bytes_per_launch": nbytes,
+                   "GB_s": nbytes / (kernel_ms[name] / launches[name] * 1e-3) / 1e9,
+                   "frac_of_hbm_peak": nbytes / (kernel_ms[name] / launches[name] * 1e-3) / 1e9 / PEAK_HBM_GBS}
+            for name, nbytes in kernel_bytes.items()
+        },
         "roofline": {
             "kernel": "bsattn_fwd_kernel",
             "bound": "mfma",
@@ -305,8 +428,8 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": traffic_bytes(),
-            "traffic_source": TRAFFIC_SUMMARY,
+            "traffic": traffic_bytes() if args.workload == "c2" else None,
+            "traffic_source": TRAFFIC_SUMMARY if args.workload == "c2" else None,
             "flops_per_launch": attn_flops_step / L,
             "min_hbm_bytes_per_launch": attn_min_bytes_step / L,
             "ms_per_launch": attn_ms_launch,

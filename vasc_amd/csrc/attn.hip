@@ -136,11 +136,6 @@ void bsattn_fwd_kernel(const AttnParams p) {
     koff[u] = static_cast<int64_t>(r) * p.k_st + c * 8;
     voff[u] = r * kHeadDim + c * 8;
   }
-  auto block_at = [&](int j, int prev) -> int {
-    if (kDense) return j;
-    const int32_t e = list[j];
-    return p.delta ? prev + e : e;
-  };
   // Issue the loads of block blk into LDS buffer buf. Full blocks take the
   // precomputed per-thread offsets from a scalar block base; the partial last
   // block clamps its rows to the sequence end (their scores are masked).
@@ -169,7 +164,11 @@ void bsattn_fwd_kernel(const AttnParams p) {
   float m = -INFINITY;  // running max in log2 units (stale by < kLazyLog2)
   float lsum = 0.f;
 
-  int blk = block_at(0, 0);
+  // List entry j+1 is loaded during iteration j-1 (index clamped to the list)
+  // so that reading it never waits on memory: the wait at the top of each
+  // iteration already covers it.
+  int blk = kDense ? 0 : __builtin_amdgcn_readfirstlane(list[0]);
+  int32_t e_next = kDense ? 0 : list[n > 1 ? 1 : 0];
   fetch(blk, 0);
   for (int j = 0; j < n; ++j) {
     const int buf = j & 1;
@@ -177,7 +176,13 @@ void bsattn_fwd_kernel(const AttnParams p) {
     __syncthreads();  // block j landed; every wave is done with buffer buf^1
     const int cur = blk;
     if (j + 1 < n) {
-      blk = block_at(j + 1, blk);
+      if (kDense) {
+        blk = j + 1;
+      } else {
+        const int e = __builtin_amdgcn_readfirstlane(e_next);
+        blk = p.delta ? blk + e : e;
+        e_next = list[j + 2 < n ? j + 2 : n - 1];
+      }
       fetch(blk, buf ^ 1);
     }
     const uint16_t *ks = smem[buf][0];
