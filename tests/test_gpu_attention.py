@@ -149,3 +149,43 @@ def test_c1_layer_topk_lists():
                                 torch.from_numpy(cnt).cuda())
     ref = OA.block_sparse_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), idx, cnt)
     _check(out, ref)
+
+
+@pytest.mark.parametrize("case", ["high", "low", "mixed"])
+def test_extreme_logits_take_the_exact_path(case):
+    """Logits far outside the fast path's range: above 64 in log2 units (the
+    block sum overflows 2^64) or all below -126 (every probability would
+    underflow). The kernel must move its exponent offset and still match the
+    float64 softmax."""
+    from vasc_amd import ops
+    B, H, nq, nk, D = 1, 2, 256, 640, 64
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(B, H, nq, D, generator=g)
+    k = torch.randn(B, H, nk, D, generator=g)
+    v = torch.randn(B, H, nk, D, generator=g)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm() * 8.0
+    if case == "high":
+        # logit std ~ 0.18 * 4 * 4 * 8 = 23: row maxima 50..105
+        q, k = q * 4.0, k * 4.0
+    else:
+        # every key ~ -4u: rows ~ +4u sit near -185 (all below -126), rows
+        # ~ -4u near +185; "mixed" interleaves those with ordinary rows
+        k = -4.0 * u + 0.5 * torch.randn(B, H, nk, D, generator=g)
+        low = 4.0 * u + 0.5 * torch.randn(B, H, nq, D, generator=g)
+        if case == "low":
+            q = low
+        else:
+            high = -4.0 * u + 0.5 * torch.randn(B, H, nq, D, generator=g)
+            r = torch.arange(nq) % 3
+            q = torch.where((r == 0).view(1, 1, nq, 1), low, torch.where((r == 1).view(1, 1, nq, 1), high, q))
+    q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    qb, nkb = math.ceil(nq / 128), math.ceil(nk / 64)
+    idx, cnt = _lists(B, H, qb, nkb, 22, density=0.6)
+    out = ops.block_sparse_attn(q.cuda(), k.cuda(), ops.pack_v(v.cuda()), torch.from_numpy(idx).cuda(),
+                                torch.from_numpy(cnt).cuda())
+    ref = OA.block_sparse_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), idx, cnt)
+    _check(out, ref)
+    dense = ops.dense_attn(q.cuda(), k.cuda(), ops.pack_v(v.cuda()))
+    dl = OA.dense_lists(B, H, nq, nk)
+    _check(dense, OA.block_sparse_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), *dl))

@@ -3,29 +3,34 @@
 // Semantics follow SpargeAttn's block-sparse kernel
 // (ZIP:csrc/qattn/qk_int_sv_f16_cuda_sm80.cuh:42-738): one workgroup per
 // (128-row query block, head, batch) walks only the 64-key blocks named by
-// its list, with an online base-2 softmax and masking of keys past the end.
-// The arithmetic is bf16 MFMA with fp32 accumulation instead of int8 QK^T +
-// fp16 PV, and the structure is CDNA4's:
+// its list, with a base-2 softmax and masking of keys past the end. The
+// arithmetic is bf16 MFMA with fp32 accumulation instead of int8 QK^T + fp16
+// PV, and the structure is CDNA4's:
 //
 //  * 4 waves x 32 query rows. S^T = K Q^T on v_mfma_f32_32x32x16_bf16 so a
-//    lane owns one query row (lane % 32) and 32 of the 64 keys: the row max
-//    and row sum are lane-local plus one xor-32 exchange.
+//    lane owns one query row (lane % 32) and 32 of the 64 keys of a block.
 //  * O^T = Vt P^T on the same MFMA, so P feeds the B operand straight from
-//    the S^T accumulators and the rescale is lane-local. Vt comes from
-//    vasc_pack_v with keys permuted into exactly the order the accumulators
-//    hold them. The row sum is taken on the bf16-rounded P with v_dot2 so the
-//    normaliser matches the P the MFMA consumes.
-//  * Lazy rescaling: the running max only moves (and O is only rescaled)
-//    when a block raises it by more than 8 in log2 units; P then stays below
-//    2^8, far inside bf16 and fp32 range, and the result is unchanged up to
-//    rounding. Most blocks skip the 32 multiplies.
-//  * K and Vt tiles arrive through global_load_lds_dwordx4 straight into a
-//    double-buffered LDS tile (2 x 16 KB), one block ahead of the MFMAs, with
-//    a 16-byte-chunk xor swizzle ((row/2)%8) that spreads the 32 rows an
-//    MFMA operand read touches over all LDS banks.
-//  * Accumulators stay in VGPRs (built with -mllvm -amdgpu-mfma-vgpr-form,
-//    no AGPR copies) and the kernel is held to 128 VGPRs so four waves share
-//    each SIMD: one wave's MFMAs overlap another's exp/VALU work.
+//    the S^T accumulators. Vt comes from vasc_pack_v with keys permuted into
+//    exactly the order the accumulators hold them.
+//  * The kernel is held to 128 VGPRs so four waves share each SIMD: one
+//    wave's MFMAs overlap other waves' exponentials (on gfx950 a v_exp_f32
+//    costs about 2.3 FMA issue slots; at head_dim 64 the exponentials cost
+//    as much VALU time as the MFMAs take).
+//  * The exponent offset m only has to keep probabilities inside fp32/bf16
+//    range, not equal the row max: softmax is invariant to it. m starts at
+//    0 and the fast path is P = exp2(fma(S, sm_scale*log2(e), -m)) on the
+//    exact fp32 logits: no max, no rescale. Each lane sums its block's bf16
+//    probabilities with v_dot2 (the sum is also the normaliser); a block sum
+//    above 2^64, or a running sum below 2^-60 (a row whose logits are all far
+//    below 0), sends the wave through an exact path that moves m to the row
+//    max and rescales O and the sum. The same path masks the keys of the
+//    partial last block and of blocks outside the sequence.
+//  * K and Vt tiles arrive by LDS DMA (global_load_lds_dwordx4) into a
+//    double-buffered LDS tile one block ahead of the MFMAs, with a
+//    16-byte-chunk xor swizzle ((row/2)%8) that spreads the rows an MFMA
+//    operand read touches over all LDS banks. The DMA is issued through asm:
+//    the compiler cannot tell a DMA into the other buffer from one into the
+//    buffer being read and would drain it before every LDS read.
 //  * workgroup ids are remapped so each XCD walks a contiguous range of
 //    query blocks of the same head (K/V reuse in that XCD's L2).
 #include "common.h"
@@ -70,13 +75,32 @@ __device__ __forceinline__ float add_bf16_pair(uint32_t pair, float acc) {
 // LDS chunk swizzle of tile row r (16-byte chunks, 8 per 128-byte row).
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
-constexpr float kLazyLog2 = 8.0f;  // rescale only when the max grows by > 2^8
+// Exact-path triggers: a lane's block sum above kHigh (a probability may be
+// near overflow) or a running sum below kLow (the row's logits are so far
+// below m that they lose precision).
+constexpr float kHigh = 18446744073709551616.0f;  // 2^64
+constexpr float kLow = 8.673617379884035e-19f;    // 2^-60
+
+// 16-byte-per-lane DMA from global memory straight into LDS: lane i's chunk
+// lands at lds_addr + 16*i (the LDS address goes through M0, which is saved
+// and restored around the load).
+__device__ __forceinline__ void lds_dma16(const void *sbase, uint32_t voff_bytes, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voff_bytes), "s"(sbase)
+      : "memory");
+}
 
 template <bool kDense>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void bsattn_fwd_kernel(const AttnParams p) {
   constexpr int CH = 512 / kThreads;  // 16-byte chunks per thread per tile
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][kTile];  // [buffer][K, Vt]
+  auto lds_u32 = [](const uint16_t *ptr) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint16_t *)ptr));
+  };
 
   const int64_t wg = xcd_remap(blockIdx.x, p.num_wg);
   const int qb = static_cast<int>(wg % p.nqb);
@@ -119,50 +143,113 @@ void bsattn_fwd_kernel(const AttnParams p) {
       qf[s] = qvalid ? *reinterpret_cast<const u32x4 *>(qptr + 16 * s + 8 * hf) : u32x4{0, 0, 0, 0};
   }
 
-  // Staging: LDS chunk ci = u*256 + tid lands at byte 16*ci (global_load_lds
-  // writes lane i of a wave at base + 16*i); it holds tile row ci/8, logical
-  // chunk (ci%8) ^ swz(row), so each lane fetches that global chunk.
+  // Staging: LDS chunk ci = u*256 + tid lands at byte 16*ci (the DMA writes
+  // lane i of a wave at base + 16*i); it holds tile row ci/8, logical chunk
+  // (ci%8) ^ swz(row), so each lane fetches that global chunk.
   const uint16_t *kbase = p.k + b * p.k_sb + h * p.k_sh;
   const uint16_t *vbase = p.vt + (bh * p.nkb) * kTile;
   const int nk32 = static_cast<int>(p.nk);
   const int nkb32 = static_cast<int>(p.nkb);
-  int64_t koff[CH];
-  int krow[CH], voff[CH];
+  const int partial = (nk32 % kBlockK) ? nkb32 - 1 : -1;  // the partial last block, if any
+  uint32_t koffb[CH], koffl[CH], voffb[CH];                 // per-lane byte offsets in a block
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
     const int ci = u * kThreads + tid;
     const int r = ci >> 3, c = (ci & 7) ^ swz(r);
-    krow[u] = r;
-    koff[u] = static_cast<int64_t>(r) * p.k_st + c * 8;
-    voff[u] = r * kHeadDim + c * 8;
+    koffb[u] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_st + c * 8) * 2);
+    voffb[u] = static_cast<uint32_t>((r * kHeadDim + c * 8) * 2);
+    // rows of the partial block past the sequence end read the last row
+    const int t = partial * kBlockK + r;
+    koffl[u] = (partial < 0 || t < nk32)
+                   ? koffb[u]
+                   : static_cast<uint32_t>(koffb[u] + static_cast<int64_t>(nk32 - 1 - t) * p.k_st * 2);
   }
-  // Issue the loads of block blk into LDS buffer buf. Full blocks take the
-  // precomputed per-thread offsets from a scalar block base; the partial last
-  // block clamps its rows to the sequence end (their scores are masked).
+  // K and Vt of block blk -> LDS buffer buf. Blocks outside [0, nkb) load
+  // block 0 (their scores are masked).
   auto fetch = [&](int blk, int buf) {
     const int sb = (blk >= 0 && blk < nkb32) ? blk : 0;
     const uint16_t *kb = kbase + static_cast<int64_t>(sb) * kBlockK * p.k_st;
     const uint16_t *vb = vbase + static_cast<int64_t>(sb) * kTile;
-    const bool full = (sb + 1) * kBlockK <= nk32;
+    const uint32_t kd = lds_u32(smem[buf][0]) + w * 64 * 16, vd = lds_u32(smem[buf][1]) + w * 64 * 16;
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-      const uint16_t *ks = kb + koff[u];
-      if (!full) {
-        const int t = sb * kBlockK + krow[u];
-        if (t >= nk32) ks = kbase + static_cast<int64_t>(nk32 - 1) * p.k_st + (koff[u] - static_cast<int64_t>(krow[u]) * p.k_st);
-      }
-      uint16_t *kd = &smem[buf][0][(u * kThreads + w * 64) * 8];
-      uint16_t *vd = &smem[buf][1][(u * kThreads + w * 64) * 8];
-      __builtin_amdgcn_global_load_lds(ks, (__attribute__((address_space(3))) void *)kd, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vb + voff[u], (__attribute__((address_space(3))) void *)vd, 16, 0, 0);
+      lds_dma16(kb, sb == partial ? koffl[u] : koffb[u], kd + u * kThreads * 16);
+      lds_dma16(vb, voffb[u], vd + u * kThreads * 16);
     }
   };
+  // Keys of block blk that exist: 64, fewer for the partial last block, 0
+  // for blocks outside [0, nkb).
+  auto valid_keys = [&](int blk) {
+    return (blk >= 0 && blk < nkb32) ? (blk == partial ? nk32 - blk * kBlockK : kBlockK) : 0;
+  };
 
-  floatx16 oacc[2];
+  const floatx16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  floatx16 oacc[2] = {zero16, zero16};
+  float ls = 0.f;  // running sum of the bf16 probabilities (this lane's 32 keys per block)
+  float m = 0.f;   // exponent offset of this lane's row (log2 units)
+  const float c = p.c;
+
+  // P = exp2(c S - m) for k-step s of the PV product (accumulators
+  // 8(s%2)..+7 of tile s/2), packed to bf16; returns bs plus the sum of the
+  // rounded pairs.
+  auto exp_step = [&](const floatx16 (&S)[2], u32x4 (&pb)[4], int s, float bs) {
+    const int t = s >> 1, r = 8 * (s & 1);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) { oacc[0][i] = 0.f; oacc[1][i] = 0.f; }
-  float m = -INFINITY;  // running max in log2 units (stale by < kLazyLog2)
-  float lsum = 0.f;
+    for (int e = 0; e < 4; ++e) {
+      const float x0 = __builtin_amdgcn_exp2f(fmaf(S[t][r + 2 * e], c, -m));
+      const float x1 = __builtin_amdgcn_exp2f(fmaf(S[t][r + 2 * e + 1], c, -m));
+      pb[s][e] = pack_bf16x2(x0, x1);
+      bs = add_bf16_pair(pb[s][e], bs);
+    }
+    return bs;
+  };
+  auto exp_block = [&](const floatx16 (&S)[2], u32x4 (&pb)[4]) {
+    float bs0 = 0.f, bs1 = 0.f;  // two partial sums: shorter dependency chains
+#pragma unroll
+    for (int s = 0; s < 4; s += 2) {
+      bs0 = exp_step(S, pb, s, bs0);
+      bs1 = exp_step(S, pb, s + 1, bs1);
+    }
+    return bs0 + bs1;
+  };
+  // Slow path for the current block: mask keys that do not exist, move m to
+  // the row max where the block left the fast path's range (both lanes of a
+  // row agree), rescale O and the sum, redo P. Rows whose running sum is
+  // negligible drop it (it holds no information relative to the new m)
+  // instead of scaling it up.
+  auto slow = [&](floatx16 (&S)[2], u32x4 (&pb)[4], int lim) {
+    if (lim < kBlockK) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
+          S[t][r] = kk < lim ? S[t][r] : -INFINITY;
+        }
+    }
+    float mx = S[0][0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, S[0][r]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[1][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = mx == -INFINITY ? mx : mx * c - m;  // block max relative to m, log2 units
+    const float lrow = ls + __shfl_xor(ls, 32);
+    const bool tiny = !(lrow >= kLow);
+    // g: how far m moves. Up to the block max when it is above m; down to it
+    // only when the row so far is negligible (or empty).
+    float g = 0.f;
+    if (mx != -INFINITY) g = (mx > 0.f || tiny) ? mx : 0.f;
+    const float alpha = tiny ? 0.f : __builtin_amdgcn_exp2f(-g);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      oacc[0][r] *= alpha;
+      oacc[1][r] *= alpha;
+    }
+    ls *= alpha;
+    m += g;
+    return exp_block(S, pb);
+  };
 
   // List entry j+1 is loaded during iteration j-1 (index clamped to the list)
   // so that reading it never waits on memory: the wait at the top of each
@@ -172,8 +259,8 @@ void bsattn_fwd_kernel(const AttnParams p) {
   fetch(blk, 0);
   for (int j = 0; j < n; ++j) {
     const int buf = j & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // block j landed; every wave is done with buffer buf^1
+    // Block j landed (every wave's share), and every wave is done with buffer buf^1.
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     const int cur = blk;
     if (j + 1 < n) {
       if (kDense) {
@@ -189,67 +276,22 @@ void bsattn_fwd_kernel(const AttnParams p) {
     const uint16_t *vs = smem[buf][1];
 
     // S^T tiles: keys 32t + [0,32) x this wave's 32 query rows.
-    floatx16 sacc[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[t][i] = 0.f;
+    floatx16 S[2];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int row = 32 * t + lr;
         const u32x4 a = *reinterpret_cast<const u32x4 *>(ks + row * kHeadDim + ((2 * s + hf) ^ swz(row)) * 8);
-        sacc[t] = mfma32(a, qf[s], sacc[t]);
+        S[t] = mfma32(a, qf[s], s == 0 ? zero16 : S[t]);
       }
 
-    // Mask keys past the sequence end and blocks outside [0, nkb).
-    const bool blk_ok = cur >= 0 && cur < nkb32;
-    const int lim = blk_ok ? nk32 - cur * kBlockK : 0;
-    if (__builtin_expect(lim < kBlockK, 0)) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
-          sacc[t][r] = kk < lim ? sacc[t][r] : -INFINITY;
-        }
-    }
-
-    float mx = fmaxf(sacc[0][0], sacc[0][1]);
-#pragma unroll
-    for (int r = 2; r < 16; ++r) mx = fmaxf(mx, sacc[0][r]);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[1][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx * p.c);
-    const bool grow = m_new > m + kLazyLog2;
-    if (__ballot(grow)) {
-      const float alpha = grow ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
-      lsum *= alpha;
-      m = grow ? m_new : m;
-    }
-    const float m_use = m == -INFINITY ? 0.f : m;
-
-    // P^T as B operand: step s uses accumulators 8(s%2)..+7 of tile s/2.
     u32x4 pb[4];
-    float ls = lsum;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int t = s >> 1, r = 8 * (s & 1);
-      uint32_t d[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x0 = __builtin_amdgcn_exp2f(fmaf(sacc[t][r + 2 * e], p.c, -m_use));
-        const float x1 = __builtin_amdgcn_exp2f(fmaf(sacc[t][r + 2 * e + 1], p.c, -m_use));
-        d[e] = pack_bf16x2(x0, x1);
-        ls = add_bf16_pair(d[e], ls);
-      }
-      pb[s] = u32x4{d[0], d[1], d[2], d[3]};
-    }
-    lsum = ls;
+    float bs = exp_block(S, pb);
+    const int lim = valid_keys(cur);
+    if (__ballot(!(bs <= kHigh) || !(ls + bs >= kLow)) || lim < kBlockK) bs = slow(S, pb, lim);
+    ls += bs;
+
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -260,7 +302,7 @@ void bsattn_fwd_kernel(const AttnParams p) {
       }
   }
 
-  const float ltot = lsum + __shfl_xor(lsum, 32);
+  const float ltot = ls + __shfl_xor(ls, 32);
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
   if (qvalid) {
 #pragma unroll
@@ -317,10 +359,8 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
   VASC_SUPPORTED(nk < (int64_t(1) << 30) && nq < (int64_t(1) << 40), "sequence of %lld keys not built (< 2^30)",
                  (long long)nk);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (dense)
-    hipLaunchKernelGGL(bsattn_fwd_kernel<true>, dim3(p.num_wg), dim3(kThreads), 0, s, p);
-  else
-    hipLaunchKernelGGL(bsattn_fwd_kernel<false>, dim3(p.num_wg), dim3(kThreads), 0, s, p);
+  auto kern = dense ? bsattn_fwd_kernel<true> : bsattn_fwd_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3(p.num_wg), dim3(kThreads), 0, s, p);
   return check_launch(dense ? "vasc_dense_attn_fwd" : "vasc_block_sparse_attn_fwd");
 }
 
