@@ -81,26 +81,12 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 constexpr float kHigh = 18446744073709551616.0f;  // 2^64
 constexpr float kLow = 8.673617379884035e-19f;    // 2^-60
 
-// 16-byte-per-lane DMA from global memory straight into LDS: lane i's chunk
-// lands at lds_addr + 16*i (the LDS address goes through M0, which is saved
-// and restored around the load).
-__device__ __forceinline__ void lds_dma16(const void *sbase, uint32_t voff_bytes, uint32_t lds_addr) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds_addr), "v"(voff_bytes), "s"(sbase)
-      : "memory");
-}
-
 template <bool kDense>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void bsattn_fwd_kernel(const AttnParams p) {
   constexpr int CH = 512 / kThreads;  // 16-byte chunks per thread per tile
   __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][kTile];  // [buffer][K, Vt]
-  auto lds_u32 = [](const uint16_t *ptr) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint16_t *)ptr));
-  };
+  auto lds_u32 = [](const uint16_t *ptr) { return lds_addr32(ptr); };
 
   const int64_t wg = xcd_remap(blockIdx.x, p.num_wg);
   const int qb = static_cast<int>(wg % p.nqb);

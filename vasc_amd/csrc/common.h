@@ -95,6 +95,33 @@ __device__ __forceinline__ int wave_sum_int(int v) {
   return v;
 }
 
+// LDS DMA: global memory straight into LDS without a register round trip.
+// Lane i of the wave writes its chunk at lds_addr + size*i. Issued through
+// asm (M0, which holds the LDS address, is saved and restored) so the
+// compiler does not see an LDS write it would drain with s_waitcnt vmcnt(0)
+// before every later LDS read: callers pace the DMA with their own vmcnt
+// waits, and a lane whose exec bit is clear loads nothing.
+__device__ __forceinline__ void lds_dma16(const void *sbase, uint32_t voff_bytes, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voff_bytes), "s"(sbase)
+      : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void *sbase, uint32_t voff_bytes, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, %3\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voff_bytes), "s"(sbase)
+      : "memory");
+}
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr32(const void *ptr) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)ptr));
+}
+
 // Maps the hardware workgroup id to a logical id so that each of the 8 XCDs
 // (which receive workgroups round-robin) processes one contiguous range of
 // logical ids, keeping neighbouring tiles of one head in one L2.

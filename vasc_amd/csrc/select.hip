@@ -8,22 +8,30 @@
 // (ZIP:spas_sage_attn/utils.py:54-87).
 //
 // Bit-exactness contract: every float32 operation below is rounded on its
-// own (contraction is off for this file) and every sum uses one of two
-// canonical float64 orders, shared with the CPU oracle:
+// own (contraction is off for this file) and every sum uses one of the
+// canonical float64 orders shared with the CPU oracle:
 //   wave sum  lane j adds elements j, j+64, ... in order, then an xor
 //             butterfly over offsets 32..1;
-//   seq sum   strictly sequential in index order;
-//   chunked   seq sums of consecutive 32-element chunks, then a seq sum of
-//             the chunk partials (the arrival mean over query rows);
-//   global    wave sum per head, then a seq sum over heads (the gate).
+//   chunked   sequential sums of consecutive 32-row chunks, then a
+//             sequential sum of the chunk partials (the arrival mean);
+//   global    wave sum per head, then sequential over heads (the gate).
 // Selection keeps the c largest priorities, ties to the lower block index.
 //
-// Launches (VASC mode): arrival (one wave per row) -> colsum (one thread per
-// pair column and 32-row chunk) -> head (ledger settlement, arrival mean,
-// admitted debt; one thread per pair column) -> select (one wave per row,
-// radix select on order-preserving uint32 keys staged in LDS) -> service.
-// Top-K mode runs the select launch alone. Every launch is short and wide:
-// no long serial chains.
+// Launches (VASC mode), each reading the fp32 score matrix once:
+//   arrival  one workgroup per (32-row chunk, head), 4-16 waves, one wave per row: the
+//            row arrives in LDS by DMA; risk total, conservative arrival and
+//            pair reductions read it there in the canonical lane order, and
+//            the chunk's float64 column partials of the pair arrival are
+//            accumulated in row order;
+//   head     per head: ledger settlement, arrival mean, pair capacity,
+//            admitted debt, the head's partials of the global gate;
+//   select   one wave per row (1-4 rows per wave), the row in LDS by DMA:
+//            priorities as order-preserving keys in place, the c-th largest
+//            key from one adaptive histogram pass plus an exact rank of the
+//            threshold bin, compaction to the ascending list, pair counts;
+//   service  QK-admission service from the pair counts.
+// Top-K mode runs the select launch alone. Every pass over a row is a short
+// rolled loop over LDS, so the code stays small for any K.
 #pragma clang fp contract(off)
 
 #include "common.h"
@@ -33,8 +41,9 @@ namespace {
 
 constexpr float kFltMax = 3.402823466e38f;
 constexpr float kFltMin = 1.175494351e-38f;
-constexpr int kRowsPerWg = 4;   // select: one row per wave, 4 rows of one head
-constexpr int kChunk = 32;      // rows per partial of the arrival mean
+constexpr int kChunk = 32;       // rows per partial of the arrival mean
+constexpr int kWaves = 4;        // waves per workgroup (both row kernels)
+constexpr int kMaxPairsPerThread = 16;  // arrival column partials per thread (P <= 16 * threads)
 
 __device__ __forceinline__ uint32_t order_key(float x) {
   uint32_t u = __float_as_uint(x);
@@ -73,7 +82,8 @@ struct SelectParams {
   int64_t width;
   int32_t *count_out;
   // workspace
-  float *total, *rowpair, *a, *adm;
+  float *total, *rowpair, *adm;
+  float2 *ia;  // (innovation, admitted debt) per pair, for the select pass
   double *part, *gate_part;
   int32_t *cap, *counts;
   int64_t nchunks;
@@ -108,78 +118,131 @@ __device__ __forceinline__ int service_gate(const SelectParams &p) {
   return (fc > 0.f) && (fu >= fw);
 }
 
-// ------------------------------------------------------------------ arrival
-// Per-row capacity when it is not given: max(topk,1), plus one when the
-// forced mixed-tail block is not already among the top-k scores (the base
-// map's row count, sparse_wrapper.py:7592-7604).
-__device__ int derived_cap(const SelectParams &p, const float *srow, int lane) {
-  int t = p.topk < 1 ? 1 : p.topk;
-  if (t > p.K) t = static_cast<int>(p.K);
-  if (!p.force_last || t >= p.K) return t;
-  const uint32_t last = order_key(srow[p.K - 1]);
-  int beat = 0;
-  for (int64_t k = lane; k < p.K; k += 64) {
-    const uint32_t key = order_key(srow[k]);
-    beat += (key > last) || (key == last && k < p.K - 1);
-  }
-  beat = wave_sum_int(beat);
-  return t + (beat >= t ? 1 : 0);
+// ------------------------------------------------------------------ rows
+// Row buffers: one per wave. The row starts at element off <= 3 and the
+// 16-byte reads of a pass end at most 3 elements past off + K.
+__host__ __device__ inline int64_t row_buf_elems(int64_t K) { return ((K + 6 + 3) / 4) * 4; }
+
+// DMA of row [srow, srow + K) into buf: element k lands at buf[off + k] with
+// off = (srow & 15) / 4, so every 16-byte chunk stays aligned. Whole chunks
+// go by 16-byte DMA; the last 1-3 floats (when the row end is not 16-byte
+// aligned) by 4-byte DMA, so nothing outside [srow & ~15, srow + K) is read.
+// The caller waits with s_waitcnt vmcnt(0).
+__device__ __forceinline__ int dma_row(const float *srow, int K, uint32_t *buf, int lane) {
+  // srow and buf are uniform over the wave; make that explicit (the DMA
+  // takes both in scalar registers).
+  const uint64_t sr = reinterpret_cast<uint64_t>(srow);
+  // (readfirstlane returns int: widen through uint32_t, never sign-extend)
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(sr >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(sr)));
+  const uintptr_t start = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
+  const uintptr_t a0 = start & ~uintptr_t(15);
+  const int off = static_cast<int>((start - a0) >> 2);
+  const int bytes = static_cast<int>(start + static_cast<uintptr_t>(K) * 4u - a0);
+  const int nchunks = bytes >> 4;
+  const char *base = reinterpret_cast<const char *>(a0);
+  const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_addr32(buf));
+  for (int c0 = 0; c0 < nchunks; c0 += 64)
+    if (c0 + lane < nchunks) lds_dma16(base, static_cast<uint32_t>(c0 + lane) * 16u, lbase + c0 * 16);
+  const int tail = (bytes - (nchunks << 4)) >> 2;  // 0..3 floats
+  if (lane < tail) lds_dma4(base + (nchunks << 4), lane * 4u, lbase + (nchunks << 4));
+  return off;
 }
 
-__global__ __launch_bounds__(256) void arrival_kernel(const SelectParams p) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= p.BH * p.Q) return;
-  const int lane = threadIdx.x & 63;
-  const int64_t bh = row / p.Q;
-  const float *srow = p.score + row * p.K;
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ------------------------------------------------------------------ arrival
+// One workgroup per (32-row chunk, head). Wave w takes rows w, w+4, ... of
+// the chunk: risk total (wave sum), conservative arrival A, pair arrival
+// a_p = (A_2p + A_2p+1) / pair_size written in place over the row (position
+// p was already consumed), its row sum (wave sum over the even positions).
+// Then thread t adds the pair values of the four rows, in row order, into
+// the float64 column partials of pairs t, t+256, ...
+__global__ __launch_bounds__(1024) void arrival_kernel(const SelectParams p, int bufn) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  __shared__ int offs[16];
+  const int nw = blockDim.x >> 6;  // waves per workgroup (4, 8 or 16)
+  const int64_t chunk = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
+  const int64_t q0 = chunk * kChunk;
+  const int nrows = static_cast<int>(p.Q - q0 < kChunk ? p.Q - q0 : kChunk);
+  const int K = static_cast<int>(p.K);
   const float *iota = p.innovation + bh * p.P;
-  const int cap = p.row_cap ? p.row_cap[row] : derived_cap(p, srow, lane);
+  uint32_t *buf = lds + w * bufn;
+  double part[kMaxPairsPerThread];
+#pragma unroll
+  for (int i = 0; i < kMaxPairsPerThread; ++i) part[i] = 0.0;
 
-  double acc = 0.0;
-  for (int64_t k = lane; k < p.K; k += 64) acc = acc + static_cast<double>(clean_score(srow[k]) * iota[k >> 1]);
-  const float total = static_cast<float>(wave_butterfly(acc));
-  const float scale = static_cast<float>(cap) / floor_tiny(total);
-
-  double racc = 0.0;
-  float *arow = p.a + row * p.P;
-  for (int64_t base = 0; base < p.K; base += 64) {
-    const int64_t k = base + lane;
-    float A = 0.f;
-    if (k < p.K && total > 0.f) A = clamp01((clean_score(srow[k]) * iota[k >> 1]) * scale);
-    const float An = __shfl_down(A, 1);
-    if (k < p.K && (lane & 1) == 0) {
-      const float ap = (k + 1 < p.K) ? (A + An) / 2.0f : (A + 0.0f) / 1.0f;
-      arow[k >> 1] = ap;
-      racc = racc + static_cast<double>(ap);
+  for (int r0 = 0; r0 < nrows; r0 += nw) {
+    const int r = r0 + w;
+    if (r < nrows) {
+      const int64_t row = bh * p.Q + q0 + r;
+      const float *srow = p.score + row * p.K;
+      const int off = dma_row(srow, K, buf, lane);
+      wait_dma();
+      const float *x = reinterpret_cast<const float *>(buf + off);
+      int cap;
+      if (p.row_cap) {
+        cap = p.row_cap[row];
+      } else {
+        cap = p.topk < 1 ? 1 : p.topk;
+        cap = cap > K ? K : cap;
+        if (p.force_last && cap < K) {
+          const uint32_t last = order_key(x[K - 1]);
+          int beat = 0;
+          for (int k = lane; k < K; k += 64) {
+            const uint32_t kk = order_key(x[k]);
+            beat += (kk > last) || (kk == last && k < K - 1);
+          }
+          cap += wave_sum_int(beat) >= cap ? 1 : 0;
+        }
+      }
+      double acc = 0.0;
+      for (int k = lane; k < K; k += 64) acc = acc + static_cast<double>(clean_score(x[k]) * iota[k >> 1]);
+      const float total = static_cast<float>(wave_butterfly(acc));
+      const float scale = static_cast<float>(cap) / floor_tiny(total);
+      double racc = 0.0;
+      float *apair = reinterpret_cast<float *>(buf + off);
+      for (int kb = 0; kb < K; kb += 64) {
+        const int k = kb + lane;
+        float A = 0.f;
+        if (k < K && total > 0.f) A = clamp01((clean_score(x[k]) * iota[k >> 1]) * scale);
+        const float An = __shfl_down(A, 1);
+        if (k < K && (lane & 1) == 0) {
+          const float ap = (k + 1 < K) ? (A + An) / 2.0f : (A + 0.0f) / 1.0f;
+          apair[k >> 1] = ap;
+          racc = racc + static_cast<double>(ap);
+        }
+      }
+      const float rowpair = static_cast<float>(wave_butterfly(racc));
+      if (lane == 0) {
+        p.total[row] = total;
+        p.rowpair[row] = rowpair;
+        p.cap[row] = cap;
+        offs[w] = off;
+      }
     }
+    __syncthreads();
+    const int rows_here = nrows - r0 < nw ? nrows - r0 : nw;
+#pragma unroll
+    for (int i = 0; i < kMaxPairsPerThread; ++i) {
+      const int64_t pp = tid + static_cast<int64_t>(blockDim.x) * i;
+      if (pp < p.P)
+        for (int rr = 0; rr < rows_here; ++rr)
+          part[i] = part[i] + static_cast<double>(__uint_as_float(lds[rr * bufn + offs[rr] + pp]));
+    }
+    __syncthreads();
   }
-  const float rowpair = static_cast<float>(wave_butterfly(racc));
-  if (lane == 0) {
-    p.total[row] = total;
-    p.rowpair[row] = rowpair;
-    p.cap[row] = cap;
+  double *out = p.part + (bh * p.nchunks + chunk) * p.P;
+#pragma unroll
+  for (int i = 0; i < kMaxPairsPerThread; ++i) {
+    const int64_t pp = tid + static_cast<int64_t>(blockDim.x) * i;
+    if (pp < p.P) out[pp] = part[i];
   }
 }
 
 // ------------------------------------------------------------------ head
-// Partial column sums of the row pair arrival over 32-row chunks.
-__global__ __launch_bounds__(256) void colsum_kernel(const SelectParams p) {
-  const int64_t pp = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t chunk = blockIdx.y, bh = blockIdx.z;
-  if (pp >= p.P) return;
-  const int64_t q0 = chunk * kChunk;
-  const int64_t q1 = q0 + kChunk < p.Q ? q0 + kChunk : p.Q;
-  const float *col = p.a + (bh * p.Q) * p.P + pp;
-  float v[kChunk];
-#pragma unroll
-  for (int i = 0; i < kChunk; ++i) v[i] = (q0 + i < q1) ? col[(q0 + i) * p.P] : 0.f;
-  double acc = 0.0;
-#pragma unroll
-  for (int i = 0; i < kChunk; ++i)
-    if (q0 + i < q1) acc = acc + static_cast<double>(v[i]);
-  p.part[(bh * p.nchunks + chunk) * p.P + pp] = acc;
-}
-
 // Per head: ledger settlement, pending arrival (mean over rows), pair
 // capacity and admitted debt. Wave 0 of every workgroup recomputes the head's
 // debt sum and pair capacity (canonical wave sums); workgroup 0 of the head
@@ -228,137 +291,306 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
   p.debt_out[bh * p.P + pp] = d;
   const float dsum = sh_dsum;
   const float scale = sh_pc / floor_tiny(dsum);
-  p.adm[bh * p.P + pp] = dsum > 0.f ? clamp01(d * scale) : 0.f;
+  const float admit = dsum > 0.f ? clamp01(d * scale) : 0.f;
+  p.adm[bh * p.P + pp] = admit;
+  p.ia[bh * p.P + pp] = float2{p.innovation[bh * p.P + pp], admit};
 }
 
 // ------------------------------------------------------------------ select
-// Wave-level radix select: returns the key T of the c-th largest element
-// (1 <= c <= K) and, through need, how many elements equal to T to keep.
-__device__ uint32_t radix_threshold(const uint32_t *keys, int64_t K, uint32_t *hist, int lane, int &need) {
-  uint32_t prefix = 0, pmask = 0;
-#pragma unroll 1
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
+// The row's keys sit in LDS, key of element k at buf[off + k]; lane l
+// visits LDS elements e = 256 it + 4 l + j (j = 0..3) with one 16-byte read.
+// Slots outside the row (e < off, e >= off + K) hold key 0, which no real
+// value maps to, so the passes below need no range checks: every threshold
+// they compare against is >= 1. Loops go `for (e = 4 lane; e < n4; e += 256)`
+// with n4 = off + K.
+
+// Wave-uniform min and max of the keys in [lo, hi).
+__device__ void range_minmax(const uint32_t *buf, int n4, int lane, uint64_t lo, uint64_t hi, uint32_t &kmin,
+                             uint32_t &kmax) {
+  uint32_t mn = 0xffffffffu, mx = 0u;
+  for (int e = 4 * lane; e < n4; e += 256) {
+    const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hist[4 * lane + i] = 0;
-    wave_sync();
-    for (int64_t k = lane; k < K; k += 64) {
-      const uint32_t key = keys[k];
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    for (int j = 0; j < 4; ++j) {
+      const bool in = x[j] >= lo && x[j] < hi;
+      mn = in && x[j] < mn ? x[j] : mn;
+      mx = in && x[j] > mx ? x[j] : mx;
     }
-    wave_sync();
-    const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
-    const int v = static_cast<int>(h0 + h1 + h2 + h3);
-    int suf = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_down(suf, off);
-      if (lane + off < 64) suf += t;
-    }
-    const uint64_t ball = __ballot(suf >= need);
-    const int L = 63 - __clzll(static_cast<long long>(ball));
-    int above = __shfl(suf - v, L);
-    int digit = 0, above_l = above;
-    if (lane == L) {
-      const uint32_t hs[4] = {h0, h1, h2, h3};
-      digit = 4 * L;
-      for (int b = 3; b >= 0; --b) {
-        if (above_l + static_cast<int>(hs[b]) >= need) {
-          digit = 4 * L + b;
-          break;
-        }
-        above_l += static_cast<int>(hs[b]);
-      }
-    }
-    digit = __shfl(digit, L);
-    above = __shfl(above_l, L);
-    need -= above;
-    prefix |= static_cast<uint32_t>(digit) << shift;
-    pmask |= 0xffu << shift;
-    wave_sync();
   }
-  return prefix;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t a = __shfl_xor(mn, o), b = __shfl_xor(mx, o);
+    mn = a < mn ? a : mn;
+    mx = b > mx ? b : mx;
+  }
+  kmin = __builtin_amdgcn_readfirstlane(mn);
+  kmax = __builtin_amdgcn_readfirstlane(mx);
 }
 
-__global__ __launch_bounds__(256) void select_kernel(const SelectParams p) {
-  extern __shared__ uint32_t lds[];
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+// The c-th largest key of the row (1 <= c < K). Each level histograms the
+// keys of the current range [kmin, kmax] into 256 bins of width 2^s (LDS
+// atomics; keys above the range are counted in `above`) and a suffix scan
+// picks the bin holding the c-th largest key. The search ends when that bin
+// is consumed whole (every key >= its lower edge is kept), when its keys are
+// all equal, or when it holds at most 64 keys: those are compacted one per
+// lane and ranked exactly with readlane compares. Otherwise the bin's own
+// [min, max] becomes the next level's range (each level shrinks the range
+// by at least 2^8). Returns T; need = how many keys equal to T to keep in
+// index order (INT_MAX: all of them) and eqT = how many keys equal T.
+__device__ uint32_t find_threshold(const uint32_t *buf, int n4, int lane, uint32_t kmin, uint32_t kmax, int c,
+                                   int n, int &need, int &eqT, uint32_t *hist) {
+  int above = 0;   // keys > kmax (outside the current range, all kept)
+  int inr = n;     // keys inside [kmin, kmax]
+#pragma unroll 1
+  for (int level = 0;; ++level) {
+    if (kmin == kmax) {  // every key of the range is equal: keep the first need of them
+      need = c - above;
+      eqT = inr;
+      return kmax;
+    }
+    const uint32_t range = kmax - kmin;
+    const int sh = 32 - __clz(range) > 8 ? 32 - __clz(range) - 8 : 0;  // (range >> sh) < 256
+    *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
+    wave_sync();
+    if (level == 0) {  // the whole row: every key but the 0 slots is in range
+      for (int e = 4 * lane; e < n4; e += 256) {
+        const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (x[j] != 0u) atomicAdd(&hist[(x[j] - kmin) >> sh], 1u);
+      }
+    } else {
+      for (int e = 4 * lane; e < n4; e += 256) {
+        const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (x[j] >= kmin && x[j] <= kmax) atomicAdd(&hist[(x[j] - kmin) >> sh], 1u);
+      }
+    }
+    wave_sync();
+    const u32x4 h = *reinterpret_cast<const u32x4 *>(hist + 4 * lane);
+    const int v = static_cast<int>(h[0] + h[1] + h[2] + h[3]);
+    int suf = v;  // keys in bins 4*lane .. 255 (inclusive suffix)
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_down(suf, o);
+      if (lane + o < 64) suf += t;
+    }
+    const int need_r = c - above;  // keys still to find inside the range
+    const int L = 63 - __clzll(static_cast<long long>(__ballot(suf >= need_r)));
+    int bin = 0, abv = 0, inb = 0;
+    if (lane == L) {
+      abv = suf - v;
+      for (int bb = 3; bb >= 0; --bb) {
+        if (abv + static_cast<int>(h[bb]) >= need_r) {
+          bin = 4 * L + bb;
+          inb = static_cast<int>(h[bb]);
+          break;
+        }
+        abv += static_cast<int>(h[bb]);
+      }
+    }
+    bin = __builtin_amdgcn_readlane(bin, L);
+    abv = __builtin_amdgcn_readlane(abv, L);
+    inb = __builtin_amdgcn_readlane(inb, L);
+    above += abv;
+    const int need_b = c - above;  // 1 <= need_b <= inb
+    const uint32_t lowT = kmin + (static_cast<uint32_t>(bin) << sh);
+    const uint64_t highT = bin == 255 ? static_cast<uint64_t>(kmax) + 1u
+                                      : static_cast<uint64_t>(kmin) + (static_cast<uint64_t>(bin + 1) << sh);
+    if (need_b == inb) {
+      need = 0x7fffffff;
+      eqT = 0;
+      return lowT;
+    }
+    if (inb <= 64) {
+      // The bin's keys, one per lane (order irrelevant), then exact ranks.
+      int n = 0;
+      for (int e = 4 * lane; e < n4; e += 256) {
+        const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool in = x[j] >= lowT && static_cast<uint64_t>(x[j]) < highT;
+          const uint64_t bal = __ballot(in);
+          if (in) hist[n + __popcll(bal & lanemask_lt())] = x[j];
+          n += __popcll(bal);
+        }
+      }
+      wave_sync();
+      const uint32_t mine = lane < inb ? hist[lane] : 0u;
+      int gt = 0, eq = 0;
+      for (int jj = 0; jj < inb; ++jj) {
+        const uint32_t x = __builtin_amdgcn_readlane(mine, jj);
+        gt += x > mine;
+        eq += x == mine;
+      }
+      const bool isT = lane < inb && gt < need_b && need_b <= gt + eq;
+      const int Lt = __builtin_ctzll(__ballot(isT));
+      need = need_b - __builtin_amdgcn_readlane(gt, Lt);
+      eqT = __builtin_amdgcn_readlane(eq, Lt);
+      return __builtin_amdgcn_readlane(mine, Lt);
+    }
+    inr = inb;
+    range_minmax(buf, n4, lane, lowT, highT, kmin, kmax);  // next level: the bin's own range
+  }
+}
+
+// One wave per row, rows_per_wave consecutive rows per wave, kWaves waves per
+// workgroup (all rows of one head). LDS: the waves' row buffers, their
+// histograms, then the workgroup's pair counts (VASC).
+template <bool kVasc>
+__global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int bufn, int rows_per_wave) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
   const int64_t bh = blockIdx.y;
-  const bool vasc = p.mode == VASC_MODE_VASC;
-  uint32_t *keys = lds + static_cast<int64_t>(w) * p.K;
-  uint32_t *hist = lds + 4 * p.K + 256 * w;
-  uint32_t *pair_cnt = lds + 4 * p.K + 1024;
-  if (vasc) {
+  uint32_t *buf = lds + w * bufn;
+  uint32_t *hist = lds + kWaves * bufn + w * 256;
+  uint32_t *pair_cnt = lds + kWaves * (bufn + 256);
+  const int K = static_cast<int>(p.K);
+  int gate = 0;
+  if (kVasc) {
     for (int64_t i = tid; i < p.P; i += 256) pair_cnt[i] = 0;
     __syncthreads();
+    gate = service_gate(p);
   }
-  const int gate = vasc ? service_gate(p) : 0;
-  const float *iota = vasc ? p.innovation + bh * p.P : nullptr;
-  const float *adm = vasc ? p.adm + bh * p.P : nullptr;
+  const float2 *ia = kVasc ? p.ia + bh * p.P : nullptr;
 
-  for (int rr = w; rr < kRowsPerWg; rr += 4) {
-    const int64_t q = static_cast<int64_t>(blockIdx.x) * kRowsPerWg + rr;
+  for (int rr = 0; rr < rows_per_wave; ++rr) {
+    const int64_t q = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * rows_per_wave + rr;
     if (q >= p.Q) break;
     const int64_t row = bh * p.Q + q;
     const float *srow = p.score + row * p.K;
+    const int off = dma_row(srow, K, buf, lane);
+    wait_dma();
+
+    // Keys in place: order_key of the score (Top-K) or of the priority (VASC).
     int c;
-    if (vasc) {
+    float total = 0.f, scale = 0.f;
+    uint32_t last = 0;
+    if (kVasc) {
       const int cap = p.cap[row];
       c = cap < p.max_capacity ? cap : p.max_capacity;
-      const float total = p.total[row];
-      const float scale = static_cast<float>(cap) / floor_tiny(total);
-      for (int64_t k = lane; k < p.K; k += 64) {
-        float A = 0.f;
-        if (total > 0.f) A = clamp01((clean_score(srow[k]) * iota[k >> 1]) * scale);
-        float prio = gate ? A + adm[k >> 1] : A;
-        if ((p.protected_mask && p.protected_mask[row * p.K + k]) || (p.force_last && k == p.K - 1)) prio = kFltMax;
-        if (p.priority_out) p.priority_out[row * p.K + k] = prio;
-        keys[k] = order_key(prio);
-      }
+      total = p.total[row];
+      scale = static_cast<float>(cap) / floor_tiny(total);
     } else {
-      c = derived_cap(p, srow, lane);
-      for (int64_t k = lane; k < p.K; k += 64) {
-        uint32_t key = order_key(srow[k]);
-        if (p.force_last && k == p.K - 1) key = 0xffffffffu;
-        keys[k] = key;
-      }
+      c = p.topk < 1 ? 1 : p.topk;
+      c = c > K ? K : c;
+      last = order_key(__uint_as_float(buf[off + K - 1]));
     }
-    c = c < 0 ? 0 : (c > p.K ? static_cast<int>(p.K) : c);
-    wave_sync();
+    const uint32_t top = order_key(kFltMax);
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+    int beat = 0;
+    const int n4 = off + K;
+    // The first and last 16-byte groups may hold slots outside the row: they
+    // become key 0.
+    for (int e = 4 * lane; e < n4; e += 256) {
+      u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = e + j - off;
+        if (k < 0 || k >= K) {
+          x[j] = 0u;
+        } else {
+          uint32_t key;
+          if (kVasc) {
+            const float2 pa = ia[k >> 1];
+            float A = 0.f;
+            if (total > 0.f) A = clamp01((clean_score(__uint_as_float(x[j])) * pa.x) * scale);
+            key = order_key(gate ? A + pa.y : A);
+            if (p.protected_mask && p.protected_mask[row * p.K + k]) key = top;
+            if (p.force_last && k == K - 1) key = top;
+          } else {
+            key = order_key(__uint_as_float(x[j]));
+            beat += (key > last) || (key == last && k < K - 1);
+            if (p.force_last && k == K - 1) key = 0xffffffffu;
+          }
+          x[j] = key;
+          kmin = key < kmin ? key : kmin;
+          kmax = key > kmax ? key : kmax;
+        }
+      }
+      *reinterpret_cast<u32x4 *>(buf + e) = x;
+    }
+    if (!kVasc && p.force_last && c < K) c += wave_sum_int(beat) >= c ? 1 : 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint32_t a = __shfl_xor(kmin, o), b = __shfl_xor(kmax, o);
+      kmin = a < kmin ? a : kmin;
+      kmax = b > kmax ? b : kmax;
+    }
+    kmin = __builtin_amdgcn_readfirstlane(kmin);
+    kmax = __builtin_amdgcn_readfirstlane(kmax);
+    c = c < 0 ? 0 : (c > K ? K : c);
+    const bool all = c >= K, none = c == 0;
+    uint32_t T = 1u;
+    int need = 0x7fffffff, eqT = 0;
+    if (none) T = 0xffffffffu;  // with `none` nothing is selected below
+    if (!all && !none) T = find_threshold(buf, n4, lane, kmin, kmax, c, K, need, eqT, hist);
+    const bool split = !all && !none && need < eqT;
+    const uint32_t tsel = all ? 1u : T;  // keys >= tsel are kept (no split); key 0 is never a row element
 
-    uint32_t T = 0;
-    int need = 0;
-    bool all = c >= p.K, none = c == 0;
-    if (!all && !none) {
-      need = c;
-      T = radix_threshold(keys, p.K, hist, lane, need);
-    }
+    // Ascending compaction: element (lane, j) of a 256-element step follows
+    // every element of lower lanes and its own j' < j.
     int32_t *irow = p.index_out + row * p.width;
-    int run_eq = 0, run_sel = 0;
-    for (int64_t base = 0; base < p.K; base += 64) {
-      const int64_t k = base + lane;
-      const bool valid = k < p.K;
-      const uint32_t key = valid ? keys[k] : 0u;
-      const bool gt = valid && (all || (!none && key > T));
-      const bool eq = valid && !all && !none && key == T;
-      const uint64_t beq = __ballot(eq);
-      const int eq_before = run_eq + __popcll(beq & lanemask_lt());
-      const bool sel = gt || (eq && eq_before < need);
-      const uint64_t bsel = __ballot(sel);
-      const int pos = run_sel + __popcll(bsel & lanemask_lt());
-      if (sel && pos < p.width) {
-        irow[pos] = static_cast<int32_t>(k);
-        if (vasc) atomicAdd(&pair_cnt[k >> 1], 1u);
+    int run_sel = 0, run_eq = 0;
+    for (int e = 4 * lane; e < n4; e += 256) {
+      const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
+      bool eq[4], sel[4];
+      uint64_t bsel[4];
+      if (split) {
+        uint64_t beq[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          eq[j] = x[j] == T;
+          beq[j] = __ballot(eq[j]);
+        }
+        int eq_rank = run_eq;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) eq_rank += __popcll(beq[j] & lanemask_lt());
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          sel[j] = x[j] > T || (eq[j] && eq_rank < need);
+          eq_rank += eq[j] ? 1 : 0;
+          run_eq += __popcll(beq[j]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sel[j] = !none && x[j] >= tsel;
       }
-      if (valid && p.mask_out) p.mask_out[row * p.K + k] = sel ? 1 : 0;
-      run_eq += __popcll(beq);
-      run_sel += __popcll(bsel);
+      int pos = run_sel;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bsel[j] = __ballot(sel[j]);
+        pos += __popcll(bsel[j] & lanemask_lt());
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = e + j - off;
+        if (sel[j]) {
+          if (pos < p.width) irow[pos] = k;
+          if (kVasc) atomicAdd(&pair_cnt[k >> 1], 1u);
+          ++pos;
+        }
+        run_sel += __popcll(bsel[j]);
+      }
+      if (p.mask_out || (kVasc && p.priority_out)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = e + j - off;
+          if (k >= 0 && k < K) {
+            if (p.mask_out) p.mask_out[row * p.K + k] = sel[j] ? 1 : 0;
+            if (kVasc && p.priority_out) p.priority_out[row * p.K + k] = __uint_as_float(x[j] & 0x7fffffffu);
+          }
+        }
+      }
     }
+    // Lanes leave the loop at different steps; lane 0 saw every step.
+    run_sel = __builtin_amdgcn_readlane(run_sel, 0);
     for (int i = lane; i < p.sink && run_sel + i < p.width; i += 64) irow[run_sel + i] = static_cast<int32_t>(p.K + i);
     if (lane == 0) p.count_out[row] = run_sel + p.sink;
-    wave_sync();
   }
-  if (vasc) {
+  if (kVasc) {
     __syncthreads();
     for (int64_t i = tid; i < p.P; i += 256) {
       const uint32_t v = pair_cnt[i];
@@ -387,23 +619,70 @@ __global__ void settle_terminal_kernel(const float *debt_in, const float *pendin
 }
 
 struct Workspace {
-  size_t total, rowpair, cap, a, adm, part, gate_part, counts, bytes;
+  size_t total, rowpair, cap, adm, ia, part, gate_part, counts, bytes;
 };
 
 Workspace layout(int64_t B, int64_t H, int64_t Q, int64_t K) {
   const size_t BH = static_cast<size_t>(B * H), P = static_cast<size_t>((K + 1) / 2);
   Workspace w;
   size_t off = 0;
-  w.total = off;   off += align256(BH * Q * 4);
-  w.rowpair = off; off += align256(BH * Q * 4);
-  w.cap = off;     off += align256(BH * Q * 4);
-  w.a = off;       off += align256(BH * Q * P * 4);
-  w.adm = off;     off += align256(BH * P * 4);
-  w.part = off;    off += align256(BH * static_cast<size_t>(cdiv(Q, kChunk)) * P * 8);
+  w.total = off;     off += align256(BH * Q * 4);
+  w.rowpair = off;   off += align256(BH * Q * 4);
+  w.cap = off;       off += align256(BH * Q * 4);
+  w.adm = off;       off += align256(BH * P * 4);
+  w.ia = off;        off += align256(BH * P * 8);
+  w.part = off;      off += align256(BH * static_cast<size_t>(cdiv(Q, kChunk)) * P * 8);
   w.gate_part = off; off += align256(BH * 3 * 8);
-  w.counts = off;  off += align256(BH * P * 4);
+  w.counts = off;    off += align256(BH * P * 4);
   w.bytes = off;
   return w;
+}
+
+int reserve_lds(const void *kern, size_t lds) {
+  if (lds <= 64 * 1024) return VASC_OK;
+  const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  if (e != hipSuccess) {
+    set_error("vasc_select_blocks: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(e));
+    return VASC_ERR_HIP;
+  }
+  return VASC_OK;
+}
+
+int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
+  const int64_t bufn = row_buf_elems(p.K);
+  int rc;
+  if (vasc) {
+    // As many waves per chunk (16, 8 or 4) as keep the row buffers within
+    // 64 KB; the column partials then need P <= 16 * (64 * waves).
+    int aw = 16;
+    while (aw > 4 && static_cast<size_t>(aw) * bufn * 4 > 64 * 1024) aw >>= 1;
+    const size_t lds = static_cast<size_t>(aw) * bufn * 4;
+    if ((rc = reserve_lds(reinterpret_cast<const void *>(arrival_kernel), lds))) return rc;
+    hipLaunchKernelGGL(arrival_kernel, dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)),
+                       dim3(64 * aw), lds, s, p, static_cast<int>(bufn));
+    if ((rc = check_launch("vasc_select_blocks/arrival"))) return rc;
+    hipLaunchKernelGGL(head_kernel, dim3(static_cast<unsigned>(cdiv(p.P, 256)), static_cast<unsigned>(p.BH)),
+                       dim3(256), 0, s, p);
+    if ((rc = check_launch("vasc_select_blocks/head"))) return rc;
+  }
+  // Rows per wave: enough waves to give every SIMD about four (1..4 rows).
+  const int64_t rows = p.BH * p.Q;
+  const int rpw = static_cast<int>(rows >= 4 * 4096 ? 4 : (rows >= 2 * 4096 ? 2 : 1));
+  const size_t lds = static_cast<size_t>(kWaves) * (bufn + 256) * 4 + (vasc ? static_cast<size_t>(p.P) * 4 : 0);
+  const void *kern = vasc ? reinterpret_cast<const void *>(select_kernel<true>)
+                          : reinterpret_cast<const void *>(select_kernel<false>);
+  if ((rc = reserve_lds(kern, lds))) return rc;
+  const dim3 grid(static_cast<unsigned>(cdiv(p.Q, static_cast<int64_t>(kWaves) * rpw)), static_cast<unsigned>(p.BH));
+  if (vasc)
+    hipLaunchKernelGGL(select_kernel<true>, grid, dim3(256), lds, s, p, static_cast<int>(bufn), rpw);
+  else
+    hipLaunchKernelGGL(select_kernel<false>, grid, dim3(256), lds, s, p, static_cast<int>(bufn), rpw);
+  if ((rc = check_launch("vasc_select_blocks/select"))) return rc;
+  if (vasc) {
+    hipLaunchKernelGGL(service_kernel, dim3(static_cast<unsigned>(cdiv(p.BH * p.P, 256))), dim3(256), 0, s, p);
+    if ((rc = check_launch("vasc_select_blocks/service"))) return rc;
+  }
+  return VASC_OK;
 }
 
 }  // namespace
@@ -424,11 +703,13 @@ extern "C" int vasc_select_blocks(const float *score, const float *innovation, i
                                   size_t workspace_bytes, void *stream) {
   using namespace vasc;
   VASC_REQUIRE(score && index_out && count_out, "score, index_out and count_out are required");
+  VASC_REQUIRE((reinterpret_cast<uintptr_t>(score) & 15) == 0, "score must be 16-byte aligned");
   VASC_REQUIRE(B > 0 && H > 0 && Q > 0 && K > 0, "sizes must be positive");
   VASC_SUPPORTED(K <= 8192, "K=%lld key blocks not built (built: <= 8192)", (long long)K);
   VASC_REQUIRE(mode == VASC_MODE_TOPK || mode == VASC_MODE_VASC, "unknown mode %d", mode);
   VASC_REQUIRE(sink_blocks >= 0, "sink_blocks must be non-negative");
   VASC_REQUIRE(B * H < 65536, "B*H too large");
+  VASC_REQUIRE(Q < (int64_t(1) << 31) / kWaves, "Q too large");
   const bool vasc = mode == VASC_MODE_VASC;
   int64_t maxc;
   if (vasc) {
@@ -478,41 +759,14 @@ extern "C" int vasc_select_blocks(const float *score, const float *innovation, i
   p.total = vasc ? reinterpret_cast<float *>(wsb + ws.total) : nullptr;
   p.rowpair = vasc ? reinterpret_cast<float *>(wsb + ws.rowpair) : nullptr;
   p.cap = vasc ? reinterpret_cast<int32_t *>(wsb + ws.cap) : nullptr;
-  p.a = vasc ? reinterpret_cast<float *>(wsb + ws.a) : nullptr;
   p.adm = vasc ? reinterpret_cast<float *>(wsb + ws.adm) : nullptr;
+  p.ia = vasc ? reinterpret_cast<float2 *>(wsb + ws.ia) : nullptr;
   p.part = vasc ? reinterpret_cast<double *>(wsb + ws.part) : nullptr;
   p.gate_part = vasc ? reinterpret_cast<double *>(wsb + ws.gate_part) : nullptr;
   p.nchunks = cdiv(Q, kChunk);
   p.counts = vasc ? reinterpret_cast<int32_t *>(wsb + ws.counts) : nullptr;
 
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t rows = p.BH * Q;
-  const size_t lds = (4 * static_cast<size_t>(K) + 1024 + (vasc ? static_cast<size_t>(p.P) : 0)) * 4;
-  VASC_SUPPORTED(lds <= 160 * 1024, "select needs %zu bytes of LDS", lds);
-  int rc;
-  if (vasc) {
-    hipLaunchKernelGGL(arrival_kernel, dim3(cdiv(rows, 4)), dim3(256), 0, s, p);
-    if ((rc = check_launch("vasc_select_blocks/arrival"))) return rc;
-    hipLaunchKernelGGL(colsum_kernel, dim3(cdiv(p.P, 256), p.nchunks, p.BH), dim3(256), 0, s, p);
-    if ((rc = check_launch("vasc_select_blocks/colsum"))) return rc;
-    hipLaunchKernelGGL(head_kernel, dim3(cdiv(p.P, 256), p.BH), dim3(256), 0, s, p);
-    if ((rc = check_launch("vasc_select_blocks/head"))) return rc;
-  }
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(select_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e != hipSuccess) {
-      set_error("vasc_select_blocks: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(e));
-      return VASC_ERR_HIP;
-    }
-  }
-  hipLaunchKernelGGL(select_kernel, dim3(cdiv(Q, kRowsPerWg), p.BH), dim3(256), lds, s, p);
-  if ((rc = check_launch("vasc_select_blocks/select"))) return rc;
-  if (vasc) {
-    hipLaunchKernelGGL(service_kernel, dim3(cdiv(p.BH * p.P, 256)), dim3(256), 0, s, p);
-    if ((rc = check_launch("vasc_select_blocks/service"))) return rc;
-  }
-  return VASC_OK;
+  return launch_rows(p, vasc, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int vasc_settle_terminal(const float *debt_in, const float *pending_arrival, const float *service,
