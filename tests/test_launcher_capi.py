@@ -76,7 +76,16 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_only_queries_and_argument_errors():
     lib = _lib.load()
-    assert lib.vasc_select_workspace_size(1, 16, 259, 518) > 16 * 259 * 259 * 4
+    # per row: total, row pair sum, capacity (fp32/int32); per pair: admitted
+    # debt, (innovation, debt) pair, service counts; per 32-row chunk and
+    # pair: a float64 partial of the arrival mean; per head: 3 gate partials.
+    def al(x):
+        return (x + 255) // 256 * 256
+    BH, Q, K = 16, 259, 518
+    P, chunks = (K + 1) // 2, -(-Q // 32)
+    expect = 3 * al(BH * Q * 4) + al(BH * P * 4) + al(BH * P * 8) + al(BH * chunks * P * 8) + al(BH * 3 * 8) \
+        + al(BH * P * 4)
+    assert lib.vasc_select_workspace_size(1, BH, Q, K) == expect
     assert lib.vasc_select_workspace_size(0, 16, 259, 518) == 0
     assert lib.vasc_packed_v_elems(1, 16, 33312, 64) == 16 * 521 * 64 * 64
     # validation happens before any HIP call: these return without a GPU
