@@ -86,3 +86,58 @@ def test_pooled_softmax(qb, kb):
     ref16 = OP.softmax(OP.pooled_logits(pq.float().numpy(), pk.float().numpy(), bf16=True))
     close = np.isclose(p16, ref16, rtol=2e-5, atol=1e-9)
     assert close.mean() > 0.999, f"{(~close).sum()} of {close.size} differ"
+
+
+def _softmax_ref(pq, pk, scale, rnd):
+    dots = np.einsum("...qd,...kd->...qk", pq.float().numpy().astype(np.float64),
+                     pk.float().numpy().astype(np.float64)).astype(np.float32)
+    if rnd:
+        logits = OP.bf16_round((OP.bf16_round(dots) * np.float32(scale)).astype(np.float32))
+    else:
+        logits = (dots.astype(np.float64) * scale).astype(np.float32)
+    return OP.softmax(logits), logits
+
+
+@pytest.mark.parametrize("case", ["huge", "tiny", "mixed"])
+def test_pooled_softmax_extreme_rows(case):
+    """Rows whose sum of exp(logit) overflows or underflows the fast pass take
+    the online (max, sum) pass; a strip without such rows stays on the fast
+    pass in the same launch."""
+    from vasc_amd import ops
+    qb, kb = 64, 200
+    g = torch.Generator().manual_seed(11)
+    pk = torch.randn(1, 2, kb, 64, generator=g) * 0.5 + 2.0  # keys share a positive direction
+    pq = torch.randn(1, 2, qb, 64, generator=g) * 0.5
+    if case == "huge":
+        pq += 12.0  # logits ~ +190: exp overflows fp32
+    elif case == "tiny":
+        pq -= 12.0  # logits ~ -190: exp underflows fp32
+    else:
+        pq[:, :, :16] += 12.0  # strip 0 partly extreme, strip 1 ordinary
+        pq[:, 1, 5] -= 24.0
+    pq, pk = pq.to(torch.bfloat16), pk.to(torch.bfloat16)
+    for rnd in (False, True):
+        got = ops.pooled_softmax(pq.cuda(), pk.cuda(), round_bf16=rnd).cpu().numpy()
+        ref, logits = _softmax_ref(pq, pk, 0.125, rnd)
+        assert np.isfinite(got).all()
+        # fp32 logits of magnitude L carry an absolute error of a few ulp(L),
+        # which becomes a relative error of the probabilities
+        rtol = 2e-5 + 16 * float(np.spacing(np.float32(np.abs(logits).max())))
+        close = np.isclose(got, ref, rtol=rtol, atol=1e-9)
+        need = 1.0 if not rnd else 0.999
+        assert close.mean() >= need, f"round={rnd}: {(~close).sum()} of {close.size} differ"
+        assert np.allclose(got.sum(-1), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("scale", [0.1, 0.125, 1.0])
+def test_pooled_softmax_scale(scale):
+    """Any scale: a power of two folds into the exp2 argument, others round twice."""
+    from vasc_amd import ops
+    qb, kb = 70, 96
+    pq, pk = _rand((1, 3, qb, 64), 21) * 2, _rand((1, 3, kb, 64), 22) * 2
+    for rnd in (False, True):
+        got = ops.pooled_softmax(pq.cuda(), pk.cuda(), scale=scale, round_bf16=rnd).cpu().numpy()
+        ref, _ = _softmax_ref(pq, pk, scale, rnd)
+        close = np.isclose(got, ref, rtol=2e-5, atol=1e-9)
+        need = 1.0 if not rnd else 0.999
+        assert close.mean() >= need, f"round={rnd}: {(~close).sum()} of {close.size} differ"
