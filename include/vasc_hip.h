@@ -74,12 +74,20 @@ int vasc_pool_qkv(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
  * i.e. the score/softmax of predict_attention (attention.py:97-101) with the
  * roundings of its bf16 autocast matmul. round_bf16 = 0 skips both
  * bfloat16 roundings. pooled_q [B,H,qb,d], pooled_k [B,H,kb,d] contiguous;
- * prob [B,H,qb,kb] float32 contiguous. Built variant: d == 64.
+ * prob [B,H,qb,kb] float32 contiguous; scale finite and > 0. workspace: at
+ * least vasc_pooled_softmax_workspace_size(B, H, qb, kb) bytes, 8-byte
+ * aligned (per-row softmax states of each 256-key block, written by a first
+ * kernel and merged by the second; no state is kept between calls).
+ * Built variant: d == 64; kb < 2^22.
  */
 int vasc_pooled_softmax(const uint16_t *pooled_q, const uint16_t *pooled_k,
                         int64_t B, int64_t H, int64_t qb, int64_t kb, int64_t d,
                         float scale, int32_t round_bf16, float *prob,
-                        void *stream);
+                        void *workspace, void *stream);
+
+/* Bytes of the vasc_pooled_softmax workspace (B*H*ceil(kb/256)*qb*8); 0 for
+ * empty shapes. Host-only. */
+int64_t vasc_pooled_softmax_workspace_size(int64_t B, int64_t H, int64_t qb, int64_t kb);
 
 /*
  * Pair innovation of given float32 pooled values [B,H,kb,d] (contiguous),

@@ -27,7 +27,8 @@ SIGNATURES: dict[str, tuple] = {
     "vasc_abi_version": (c_int32, []),
     "vasc_pool_qkv": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64,
                                 I64, I64, I64, I64, I64, I64, I64, P, P, P, P, P]),
-    "vasc_pooled_softmax": (c_int32, [P, P, I64, I64, I64, I64, I64, c_float, I32, P, P]),
+    "vasc_pooled_softmax": (c_int32, [P, P, I64, I64, I64, I64, I64, c_float, I32, P, P, P]),
+    "vasc_pooled_softmax_workspace_size": (I64, [I64, I64, I64, I64]),
     "vasc_pair_innovation": (c_int32, [P, I64, I64, I64, I64, P, P]),
     "vasc_select_workspace_size": (c_size_t, [I64, I64, I64, I64]),
     "vasc_select_blocks": (c_int32, [P, P, I64, I64, I64, I64, I32, I32, P, P, I32, I32, I32,

@@ -20,7 +20,6 @@
 // _mean_pool_contiguous_value_blocks (sparse_wrapper.py:2839-2861),
 // pair innovation (sparse_wrapper.py:3733-3740).
 #include <cmath>
-#include <type_traits>
 
 #include "innovation.h"
 
@@ -151,16 +150,10 @@ __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-constexpr int kSoftmaxWaves = 8;  // key tiles of one 32-row strip spread over 8 waves
 constexpr float kLog2e = 1.44269504088896341f;
-// A row whose sum of exp2(y) over its keys lies in [kSumLow, kSumHigh] took
-// no overflowed term and keeps full relative precision, so the fast pass
-// (no running max) is exact enough; any other row sends the strip through
-// the online (max, sum) pass.
-constexpr float kSumHigh = 0x1p100f, kSumLow = 0x1p-60f;
 
 // How the fp32 MFMA dot turns into the logit; y = r * sc is the exp2
-// argument (logit * log2 e).
+// argument (logit * log2 e), sc > 0.
 enum LogitMode : int {
   kRoundPow2 = 0,  // bf16(bf16(dot) * scale) with scale a power of two: = bf16(dot) * scale exactly
   kRoundAny = 1,   // bf16(bf16(dot) * scale)
@@ -185,141 +178,20 @@ __device__ __forceinline__ void dots_to_r(floatx16 &acc, float scale) {
   }
 }
 
-// B operand of the 32-key tile whose first key is key0 (lane: key
-// key0 + lr, dims 16s + 8hf .. +7), key clamped into [0, kb).
-__device__ __forceinline__ void load_keys(const uint16_t *kbase, int64_t key, int hf, u32x4 (&b)[4]) {
-  const uint16_t *kr = kbase + key * kHeadDim + 8 * hf;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) b[s] = *reinterpret_cast<const u32x4 *>(kr + 16 * s);
-}
-
-__device__ __forceinline__ floatx16 tile_dots(const u32x4 (&qa)[4], const u32x4 (&b)[4]) {
+__device__ __forceinline__ floatx16 tile_dots(const u32x4 (&a)[4], const u32x4 (&b)[4]) {
   floatx16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.f;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) acc = mfma32(qa[s], b[s], acc);
+  for (int s = 0; s < 4; ++s) acc = mfma32(a[s], b[s], acc);
   return acc;
 }
 
-// Strip row held by acc[r] of a lane in half hf (standard 32x32 MFMA output).
+// Row (A-operand index) held by acc[r] of a lane in half hf of the 32x32
+// MFMA output; the lane's column is its index mod 32.
 __device__ __forceinline__ int acc_row(int r, int hf) { return 8 * (r >> 2) + 4 * hf + (r & 3); }
 
-struct SoftmaxStrip {
-  const uint16_t *kbase;
-  float *out;  // row0 of the strip
-  int64_t kb, nfull, rows;  // keys, full 32-key tiles, valid rows of the strip (1..32)
-  float scale, sc;
-  int w, lr, hf;
-};
-
-// exp2(y) of one tile into the lane's 16 row sums (fast pass).
-template <int kMode, bool kMasked>
-__device__ __forceinline__ void sum_tile(const SoftmaxStrip &st, const u32x4 (&qa)[4], const u32x4 (&b)[4], int64_t t,
-                                         float (&sum)[16]) {
-  floatx16 acc = tile_dots(qa, b);
-  dots_to_r<kMode>(acc, st.scale);
-  const bool ok = !kMasked || 32 * t + st.lr < st.kb;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const float e = __builtin_amdgcn_exp2f(acc[r] * st.sc);
-    sum[r] += ok ? e : 0.f;
-  }
-}
-
-// Online (max, sum) of y over one tile (exact pass).
-template <int kMode, bool kMasked>
-__device__ __forceinline__ void online_tile(const SoftmaxStrip &st, const u32x4 (&qa)[4], const u32x4 (&b)[4],
-                                            int64_t t, float (&m)[16], float (&sum)[16]) {
-  floatx16 acc = tile_dots(qa, b);
-  dots_to_r<kMode>(acc, st.scale);
-  const bool ok = !kMasked || 32 * t + st.lr < st.kb;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const float y = acc[r] * st.sc;
-    const float d = y - m[r];
-    const bool up = d > 0.f;  // false for NaN
-    const float e = __builtin_amdgcn_exp2f(up ? -d : d);
-    const float s_up = m[r] == -INFINITY ? 1.f : fmaf(sum[r], e, 1.f);
-    if (ok) {
-      sum[r] = up ? s_up : sum[r] + e;
-      m[r] = up ? y : m[r];
-    }
-  }
-}
-
-// Normalised probabilities of one tile: exp2(y - gm) * inv.
-template <int kMode, bool kExact, bool kMasked>
-__device__ __forceinline__ void store_tile(const SoftmaxStrip &st, const u32x4 (&qa)[4], const u32x4 (&b)[4],
-                                           int64_t t, const float (&gm)[16], const float (&inv)[16],
-                                           __amdgpu_buffer_rsrc_t rsrc, const uint32_t (&soff)[16]) {
-  floatx16 acc = tile_dots(qa, b);
-  dots_to_r<kMode>(acc, st.scale);
-  if (!kMasked) {
-    const uint32_t voff = static_cast<uint32_t>((4 * st.hf * st.kb + 32 * t + st.lr) * 4);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float y = kExact ? acc[r] * st.sc - gm[r] : acc[r] * st.sc;  // y rounded as in pass 1
-      const float pr = __builtin_amdgcn_exp2f(y) * inv[r];
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pr), rsrc, voff, soff[r], 0);
-    }
-  } else {
-    // Invalid lanes get a vector offset of 2^31, past the buffer's end
-    // (num_records < 2^31) whether or not the scalar row offset is added
-    // (it is below 2^31): the store is dropped.
-    const int64_t key = 32 * t + st.lr;
-    const uint32_t voff = static_cast<uint32_t>((4 * st.hf * st.kb + key) * 4);
-    const bool kok = key < st.kb;
-    const int rlim = static_cast<int>(st.rows) - 4 * st.hf;  // acc_row(r, hf) < rows <=> acc_row(r, 0) < rlim
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float y = kExact ? acc[r] * st.sc - gm[r] : acc[r] * st.sc;  // y rounded as in pass 1
-      const bool ok = kok && acc_row(r, 0) < rlim;
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(__builtin_amdgcn_exp2f(y) * inv[r]), rsrc,
-                                            ok ? voff : 0x80000000u, soff[r], 0);
-    }
-  }
-}
-
-template <bool kMasked>
-using Masked = std::integral_constant<bool, kMasked>;
-
-// Calls f(keys, t, Masked<...>) for the wave's tiles t = w, w + 8, ... in
-// order, the last (partial) tile masked. The B operand of the next tile is
-// loaded into the other register set before the current tile's work (no
-// copies, so the load stays in flight during that work).
-template <class F>
-__device__ __forceinline__ void walk_tiles(const SoftmaxStrip &st, int64_t first_key, F &&f) {
-  constexpr int kW = kSoftmaxWaves;
-  u32x4 k0[4], k1[4];
-  int64_t t = st.w;
-  load_keys(st.kbase, first_key, st.hf, k0);
-  // Pairs of tiles with no exit between them, so neither load can be sunk
-  // next to its use.
-  while (t + kW < st.nfull) {
-    load_keys(st.kbase, 32 * (t + kW) + st.lr, st.hf, k1);
-    __builtin_amdgcn_sched_barrier(0);
-    f(k0, t, Masked<false>{});
-    __builtin_amdgcn_sched_barrier(0);
-    const int64_t n0 = t + 2 * kW < st.nfull ? t + 2 * kW : t + kW;
-    load_keys(st.kbase, 32 * n0 + st.lr, st.hf, k0);
-    __builtin_amdgcn_sched_barrier(0);
-    f(k1, t + kW, Masked<false>{});
-    __builtin_amdgcn_sched_barrier(0);
-    t += 2 * kW;
-  }
-  if (t < st.nfull) {
-    f(k0, t, Masked<false>{});
-    t += kW;
-  }
-  if (st.nfull * 32 < st.kb && t == st.nfull) {
-    const int64_t key = 32 * t + st.lr;
-    load_keys(st.kbase, key < st.kb ? key : st.kb - 1, st.hf, k0);
-    f(k0, t, Masked<true>{});
-  }
-}
-
-// (m, s) <- merge of two online-softmax states (max, sum of exp2(y - max)).
+// (m, s) <- merge of two softmax states (max y, sum of exp2(y - max)).
 __device__ __forceinline__ void merge_ms(float &m, float &s, float m2, float s2) {
   const float mn = fmaxf(m, m2);
   if (mn == -INFINITY) return;
@@ -328,142 +200,204 @@ __device__ __forceinline__ void merge_ms(float &m, float &s, float m2, float s2)
   m = mn;
 }
 
-// Pass 2 of a wave: its tiles' normalised probabilities. kExact applies the
-// per-row max (online pass) and the row mask of a partial strip.
-template <int kMode, bool kExact>
-__device__ __forceinline__ void write_pass(const SoftmaxStrip &st, const u32x4 (&qa)[4], int64_t first_key,
-                                           const float *fin_m, const float *fin_inv) {
-  float gm[16], inv[16];
-  uint32_t soff[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    gm[r] = kExact ? fin_m[acc_row(r, st.hf)] : 0.f;
-    inv[r] = fin_inv[acc_row(r, st.hf)];
-    soff[r] = static_cast<uint32_t>(acc_row(r, 0) * st.kb * 4);
-  }
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(st.out, 0, static_cast<int>(st.rows * st.kb * 4), 0x00020000);
-  walk_tiles(st, first_key, [&](const u32x4(&b)[4], int64_t t, auto masked) {
-    // the exact variant (rare: extreme rows or the partial last strip)
-    // always takes the masked store
-    constexpr bool kM = decltype(masked)::value || kExact;
-    store_tile<kMode, kExact, kM>(st, qa, b, t, gm, inv, rsrc, soff);
-  });
+// Both kernels work on blocks of 128 query rows x 256 keys of one head.
+// Wave w of a block owns keys 32w .. 32w + 31 and keeps their pooled K rows
+// in registers (the 32x32x16 A and B operands share one register layout:
+// lane l holds row l % 32, dims 8 (l / 32) + 16 s .. + 7 in register s);
+// the block's 128 pooled Q rows are staged in LDS with their 16-byte chunks
+// XOR-swizzled by row, so the 32 rows a wave reads at once hit distinct
+// banks. K and Q are read once per block.
+constexpr int kBlockRows = 128, kBlockWaves = 8, kBlockKeys = 32 * kBlockWaves;
+
+struct BlockParams {
+  const uint16_t *pq, *pk;
+  float2 *part;  // [B*H][nkb][qb] per-block row states (max y, sum exp2(y - max))
+  float *prob;
+  int64_t qb, kb, nrb, nkb, num_wg;
+  float scale, sc;
+};
+
+struct BlockCoords {
+  int64_t bh, R0, key0;  // head, first row, first key of the wave
+  int rows, nkeys;       // valid rows of the block (1..128), valid keys of the wave (<= 0: none)
+  int64_t kbk;
+};
+
+// Block of this workgroup; workgroups are ordered so that each XCD walks a
+// contiguous run of (head, row block) pairs, key blocks innermost.
+__device__ __forceinline__ BlockCoords block_coords(const BlockParams &p, int w) {
+  BlockCoords c;
+  const int64_t wg = xcd_remap(blockIdx.x, p.num_wg);
+  c.kbk = wg % p.nkb;
+  const int64_t rest = wg / p.nkb;
+  c.bh = rest / p.nrb;
+  c.R0 = (rest % p.nrb) * kBlockRows;
+  c.rows = static_cast<int>(p.qb - c.R0 < kBlockRows ? p.qb - c.R0 : kBlockRows);
+  c.key0 = c.kbk * kBlockKeys + 32 * w;
+  const int64_t nk = p.kb - c.key0;
+  c.nkeys = static_cast<int>(nk < 32 ? (nk > 0 ? nk : 0) : 32);
+  return c;
 }
 
-// One workgroup per (32-row strip, head); the workgroup walks the strip's
-// key tiles twice, wave w taking tiles w, w + 8, ...:
-//   pass 1 sums exp2(y) per row with no running max; rows whose sum falls
-//          outside [kSumLow, kSumHigh] send the whole strip through an exact
-//          online (max, sum) pass instead;
-//   pass 2 recomputes each tile and writes exp2(y - max) / sum, a wave's
-//          store covering two rows of 32 consecutive keys.
-// Workgroups are ordered so that each XCD walks the strips of a contiguous
-// run of heads (the heads' pooled K stays in that XCD's L2).
+// Stage the block's pooled Q rows (zero past qb) into qs (all threads).
+__device__ __forceinline__ void stage_q(const BlockParams &p, const BlockCoords &c, uint16_t *qs, int tid) {
+  for (int i = tid; i < kBlockRows * 8; i += kBlockWaves * 64) {
+    const int row = i >> 3, ch = i & 7;
+    u32x4 v = {0, 0, 0, 0};
+    if (row < c.rows) v = *reinterpret_cast<const u32x4 *>(p.pq + (c.bh * p.qb + c.R0 + row) * kHeadDim + 8 * ch);
+    *reinterpret_cast<u32x4 *>(qs + row * kHeadDim + 8 * (ch ^ (row & 7))) = v;
+  }
+}
+
+// Operand registers of the wave's 32 keys (key clamped into [0, kb)).
+__device__ __forceinline__ void load_key_tile(const BlockParams &p, const BlockCoords &c, int lr, int hf,
+                                              u32x4 (&k)[4]) {
+  const int64_t key = lr < c.nkeys ? c.key0 + lr : c.key0;
+  const uint16_t *kr = p.pk + (c.bh * p.kb + key) * kHeadDim + 8 * hf;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) k[s] = *reinterpret_cast<const u32x4 *>(kr + 16 * s);
+}
+
+// Operand registers of staged Q rows 32 j .. 32 j + 31.
+__device__ __forceinline__ void read_q_tile(const uint16_t *qs, int j, int lr, int hf, u32x4 (&q)[4]) {
+  const int row = 32 * j + lr;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) q[s] = *reinterpret_cast<const u32x4 *>(qs + row * kHeadDim + 8 * ((2 * s + hf) ^ (row & 7)));
+}
+
+// Per-block row states. The wave computes S^T = K Q^T (lane = query row,
+// its 16 accumulators = 16 of the wave's keys), takes the lane's max y and
+// sum of exp2(y - max) over those keys, merges the two halves (the other 16
+// keys) and then the 8 waves through LDS, and writes (max, sum) of every
+// row over the block's 256 keys.
 template <int kMode>
-__global__ __launch_bounds__(kSoftmaxWaves * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void pooled_softmax_kernel(const uint16_t *__restrict__ pq,
-                                                                           const uint16_t *__restrict__ pk,
-                                                                           int64_t qb, int64_t kb, int64_t nstrip,
-                                                                           int64_t num_wg, float scale,
-                                                                           float *__restrict__ prob) {
-  __shared__ float part[kSoftmaxWaves][32][32];
-  __shared__ float sm_m[kSoftmaxWaves][32], sm_s[kSoftmaxWaves][32];
-  __shared__ float fin_m[32], fin_inv[32];
-  __shared__ int slow_flag;
-  const int64_t wg = xcd_remap(blockIdx.x, num_wg);
-  const int64_t bh = wg / nstrip, row0 = (wg % nstrip) * 32;
-  const int tid = threadIdx.x, l = tid & 63;
-  SoftmaxStrip st;
-  st.lr = l & 31;
-  st.hf = l >> 5;
-  st.w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  st.kb = kb;
-  st.nfull = kb / 32;
-  st.rows = qb - row0 < 32 ? qb - row0 : 32;
-  st.scale = scale;
-  st.sc = kMode == kRoundAny ? kLog2e : scale * kLog2e;
-  st.kbase = pk + bh * kb * kHeadDim;
-  st.out = prob + (bh * qb + row0) * kb;
-  if (tid == 0) slow_flag = 0;
-  // A operand: lane holds query row row0 + lr, dims 16s + 8hf .. +7.
-  u32x4 qa[4];
-  {
-    const bool qok = st.lr < st.rows;
-    const uint16_t *qr = pq + (bh * qb + row0 + (qok ? st.lr : 0)) * kHeadDim + 8 * st.hf;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qa[s] = qok ? *reinterpret_cast<const u32x4 *>(qr + 16 * s) : u32x4{0, 0, 0, 0};
-  }
-  const bool tail = st.nfull * 32 < kb;
-  // first key the wave loads (in bounds even when it has no full tile)
-  int64_t first_key = 32 * (st.w < st.nfull ? st.w : st.nfull - 1) + st.lr;
-  if (first_key < 0 || first_key >= kb) first_key = kb - 1;
-
-  // ---- pass 1 (fast): per-lane row sums of exp2(y)
-  float sum[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) sum[r] = 0.f;
-  walk_tiles(st, first_key, [&](const u32x4(&b)[4], int64_t t, auto masked) {
-    sum_tile<kMode, decltype(masked)::value>(st, qa, b, t, sum);
-  });
-#pragma unroll
-  for (int r = 0; r < 16; ++r) part[st.w][acc_row(r, st.hf)][st.lr] = sum[r];
+__global__ __launch_bounds__(kBlockWaves * 64) void pooled_stats_kernel(const BlockParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t qs[kBlockRows * kHeadDim];
+  __shared__ float wm[kBlockWaves][kBlockRows], wsum[kBlockWaves][kBlockRows];
+  const int tid = threadIdx.x, l = tid & 63, lr = l & 31, hf = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const BlockCoords c = block_coords(p, w);
+  stage_q(p, c, qs, tid);
+  u32x4 kt[4];
+  if (c.nkeys > 0) load_key_tile(p, c, lr, hf, kt);
   __syncthreads();
-  {
-    // 16 threads per row: each adds 16 partials, then a 16-lane reduction.
-    const int row = tid >> 4, j = tid & 15;
-    float v = 0.f;
+  if (c.nkeys > 0) {
+    for (int j = 0; j < kBlockRows / 32; ++j) {
+      if (32 * j >= c.rows) break;
+      u32x4 qt[4];
+      read_q_tile(qs, j, lr, hf, qt);
+      floatx16 acc = tile_dots(kt, qt);
+      dots_to_r<kMode>(acc, p.scale);
+      if (c.nkeys < 32) {
 #pragma unroll
-    for (int w = 0; w < kSoftmaxWaves; ++w) v += part[w][row][j] + part[w][row][j + 16];
+        for (int r = 0; r < 16; ++r) acc[r] = acc_row(r, hf) < c.nkeys ? acc[r] : -INFINITY;
+      }
+      float mr = acc[0];
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 16);
-    if (j == 0) {
-      fin_m[row] = 0.f;
-      fin_inv[row] = 1.f / v;
-      if (row < st.rows && !(v >= kSumLow && v <= kSumHigh)) slow_flag = 1;
-    }
-  }
-  __syncthreads();
-  const bool exact = slow_flag != 0;
-
-  if (exact) {
-    // ---- pass 1 (exact): online (max, sum) per lane and row
-    float m[16];
+      for (int r = 1; r < 16; ++r) mr = fmaxf(mr, acc[r]);
+      float m = mr * p.sc, s = 0.f;
+      if (m != -INFINITY) {
+        float e[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      m[r] = -INFINITY;
-      sum[r] = 0.f;
-    }
-    walk_tiles(st, first_key, [&](const u32x4(&b)[4], int64_t t, auto masked) {
-      online_tile<kMode, decltype(masked)::value>(st, qa, b, t, m, sum);
-    });
+        for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(fmaf(acc[r], p.sc, -m));
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < 16; r += 2) e[r] += e[r + 1];
 #pragma unroll
-      for (int o = 1; o < 32; o <<= 1) merge_ms(m[r], sum[r], __shfl_xor(m[r], o), __shfl_xor(sum[r], o));
-    }
-    if (st.lr == 0) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sm_m[st.w][acc_row(r, st.hf)] = m[r];
-        sm_s[st.w][acc_row(r, st.hf)] = sum[r];
+        for (int r = 0; r < 16; r += 4) e[r] += e[r + 2];
+        s = (e[0] + e[4]) + (e[8] + e[12]);
+      }
+      merge_ms(m, s, __shfl_xor(m, 32), __shfl_xor(s, 32));
+      if (hf == 0) {
+        wm[w][32 * j + lr] = m;
+        wsum[w][32 * j + lr] = s;
       }
     }
-    __syncthreads();
-    if (tid < 32) {
-      float gm = sm_m[0][tid], gs = sm_s[0][tid];
-#pragma unroll
-      for (int i = 1; i < kSoftmaxWaves; ++i) merge_ms(gm, gs, sm_m[i][tid], sm_s[i][tid]);
-      fin_m[tid] = gm;
-      fin_inv[tid] = gs > 0.f ? 1.f / gs : 0.f;
-    }
-    __syncthreads();
   }
+  __syncthreads();
+  if (tid < c.rows) {
+    const int nw = static_cast<int>((p.kb - c.kbk * kBlockKeys + 31) / 32);  // waves with keys
+    float m = wm[0][tid], s = wsum[0][tid];
+    for (int i = 1; i < (nw < kBlockWaves ? nw : kBlockWaves); ++i) merge_ms(m, s, wm[i][tid], wsum[i][tid]);
+    p.part[(c.bh * p.nkb + c.kbk) * p.qb + c.R0 + tid] = float2{m, s};
+  }
+}
 
-  // ---- pass 2: normalised write
-  if (exact || st.rows < 32)
-    write_pass<kMode, true>(st, qa, first_key, fin_m, fin_inv);
-  else
-    write_pass<kMode, false>(st, qa, first_key, fin_m, fin_inv);
+// Normalised probabilities: merges the row states of the nkb key blocks
+// into (max, 1 / sum) per row, then wave w walks the block's four 32-row
+// tiles with its keys' operand in registers and writes
+// exp2(y - max) / sum; a store covers two rows of 32 consecutive keys.
+template <int kMode>
+__global__ __launch_bounds__(kBlockWaves * 64) void pooled_prob_kernel(const BlockParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t qs[kBlockRows * kHeadDim];
+  __shared__ __attribute__((aligned(16))) float sgm[kBlockRows], sinv[kBlockRows];
+  const int tid = threadIdx.x, l = tid & 63, lr = l & 31, hf = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const BlockCoords c = block_coords(p, w);
+  stage_q(p, c, qs, tid);
+  {
+    // 4 threads per row, each merging every 4th key block's state
+    const int row = tid >> 2, q4 = tid & 3;
+    float m = -INFINITY, s = 0.f;
+    if (row < c.rows) {
+      const float2 *pr = p.part + c.bh * p.nkb * p.qb + c.R0 + row;
+      for (int64_t i0 = q4; i0 < p.nkb; i0 += 16) {
+        // the four loads are issued together, then merged
+        float2 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = i0 + 4 * k < p.nkb ? pr[(i0 + 4 * k) * p.qb] : float2{-INFINITY, 0.f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) merge_ms(m, s, v[k].x, v[k].y);
+      }
+    }
+    merge_ms(m, s, __shfl_xor(m, 1), __shfl_xor(s, 1));
+    merge_ms(m, s, __shfl_xor(m, 2), __shfl_xor(s, 2));
+    if (q4 == 0) {
+      sgm[row] = m;
+      sinv[row] = s > 0.f ? 1.f / s : 0.f;
+    }
+  }
+  u32x4 kt[4];
+  if (c.nkeys > 0) load_key_tile(p, c, lr, hf, kt);
+  __syncthreads();
+  if (c.nkeys <= 0) return;
+  const bool full = c.nkeys == 32 && c.rows == kBlockRows;
+  const int kb = static_cast<int>(p.kb);
+  float *base = p.prob + (c.bh * p.qb + c.R0) * p.kb + c.key0;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      base, 0, static_cast<int>((static_cast<int64_t>(c.rows - 1) * p.kb + c.nkeys) * 4), 0x00020000);
+  uint32_t soff[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) soff[r] = static_cast<uint32_t>(acc_row(r, 0) * kb * 4);
+  const bool kok = lr < c.nkeys;
+  for (int j = 0; j < kBlockRows / 32; ++j) {
+    if (32 * j >= c.rows) break;
+    u32x4 qt[4];
+    read_q_tile(qs, j, lr, hf, qt);
+    floatx16 acc = tile_dots(qt, kt);  // lane = key, accumulators = rows
+    dots_to_r<kMode>(acc, p.scale);
+    float gm[16], inv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const floatx4 m4 = *reinterpret_cast<const floatx4 *>(sgm + 32 * j + 8 * g + 4 * hf);
+      const floatx4 i4 = *reinterpret_cast<const floatx4 *>(sinv + 32 * j + 8 * g + 4 * hf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gm[4 * g + e] = m4[e];
+        inv[4 * g + e] = i4[e];
+      }
+    }
+    const uint32_t voff = static_cast<uint32_t>(((32 * j + 4 * hf) * kb + lr) * 4);
+    // row 32 j + acc_row(r, hf) < rows <=> acc_row(r, 0) < rlim
+    const int rlim = c.rows - 32 * j - 4 * hf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pr = __builtin_amdgcn_exp2f(fmaf(acc[r], p.sc, -gm[r])) * inv[r];
+      // invalid lanes get a vector offset of 2^31, past the buffer's end
+      // (below 2^31) with or without the scalar row offset: the store is dropped
+      const bool ok = full || (kok && acc_row(r, 0) < rlim);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pr), rsrc, ok ? voff : 0x80000000u, soff[r], 0);
+    }
+  }
 }
 
 }  // namespace
@@ -530,26 +464,49 @@ extern "C" int vasc_pair_innovation(const float *pooled_v, int64_t B, int64_t H,
   return check_launch("vasc_pair_innovation");
 }
 
+extern "C" int64_t vasc_pooled_softmax_workspace_size(int64_t B, int64_t H, int64_t qb, int64_t kb) {
+  using namespace vasc;
+  return B > 0 && H > 0 && qb > 0 && kb > 0 ? B * H * cdiv(kb, kBlockKeys) * qb * 8 : 0;
+}
+
 extern "C" int vasc_pooled_softmax(const uint16_t *pooled_q, const uint16_t *pooled_k, int64_t B, int64_t H,
                                    int64_t qb, int64_t kb, int64_t d, float scale, int32_t round_bf16, float *prob,
-                                   void *stream) {
+                                   void *workspace, void *stream) {
   using namespace vasc;
   VASC_SUPPORTED(d == 64, "head_dim %lld not built (built: 64)", (long long)d);
-  VASC_REQUIRE(pooled_q && pooled_k && prob && B > 0 && H > 0 && qb > 0 && kb > 0, "invalid arguments");
-  VASC_REQUIRE((reinterpret_cast<uintptr_t>(pooled_q) & 15) == 0 && (reinterpret_cast<uintptr_t>(pooled_k) & 15) == 0,
-               "pooled inputs must be 16-byte aligned");
-  // one strip's output (32 rows x kb fp32) is addressed with 32-bit offsets
-  VASC_REQUIRE(kb < (int64_t(1) << 24), "kb %lld not below 2^24", (long long)kb);
-  const int64_t nstrip = cdiv(qb, 32), num_wg = nstrip * B * H;
-  VASC_REQUIRE(num_wg < (int64_t(1) << 31), "grid too large");
+  VASC_REQUIRE(pooled_q && pooled_k && prob && workspace && B > 0 && H > 0 && qb > 0 && kb > 0,
+               "invalid arguments (pooled_q, pooled_k, prob and workspace are required)");
+  VASC_REQUIRE(std::isfinite(scale) && scale > 0.f, "scale must be finite and positive");
+  VASC_REQUIRE((reinterpret_cast<uintptr_t>(pooled_q) & 15) == 0 && (reinterpret_cast<uintptr_t>(pooled_k) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(workspace) & 7) == 0,
+               "pooled inputs must be 16-byte aligned, the workspace 8-byte aligned");
+  // a probability block (128 rows x kb fp32) is addressed with 32-bit offsets
+  VASC_REQUIRE(kb < (int64_t(1) << 22), "kb %lld not below 2^22", (long long)kb);
+  BlockParams p;
+  p.pq = pooled_q;
+  p.pk = pooled_k;
+  p.part = static_cast<float2 *>(workspace);
+  p.prob = prob;
+  p.qb = qb;
+  p.kb = kb;
+  p.nrb = cdiv(qb, kBlockRows);
+  p.nkb = cdiv(kb, kBlockKeys);
+  p.num_wg = p.nrb * p.nkb * B * H;
+  VASC_REQUIRE(p.num_wg < (int64_t(1) << 31), "grid too large");
   int e = 0;
-  const bool pow2 = std::isfinite(scale) && scale != 0.f && std::frexp(scale, &e) == 0.5f;
+  const bool pow2 = std::frexp(scale, &e) == 0.5f;
   const int mode = !round_bf16 ? kFp32 : pow2 ? kRoundPow2 : kRoundAny;
-  auto kern = mode == kRoundPow2 ? pooled_softmax_kernel<kRoundPow2>
-              : mode == kRoundAny ? pooled_softmax_kernel<kRoundAny>
-                                  : pooled_softmax_kernel<kFp32>;
-  hipLaunchKernelGGL(kern, dim3(num_wg), dim3(kSoftmaxWaves * 64), 0, reinterpret_cast<hipStream_t>(stream), pooled_q,
-                     pooled_k, qb, kb, nstrip, num_wg, scale, prob);
+  p.scale = scale;
+  p.sc = mode == kRoundAny ? kLog2e : scale * kLog2e;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto ks = mode == kRoundPow2 ? pooled_stats_kernel<kRoundPow2>
+            : mode == kRoundAny ? pooled_stats_kernel<kRoundAny>
+                                : pooled_stats_kernel<kFp32>;
+  hipLaunchKernelGGL(ks, dim3(p.num_wg), dim3(kBlockWaves * 64), 0, st, p);
+  auto kp = mode == kRoundPow2 ? pooled_prob_kernel<kRoundPow2>
+            : mode == kRoundAny ? pooled_prob_kernel<kRoundAny>
+                                : pooled_prob_kernel<kFp32>;
+  hipLaunchKernelGGL(kp, dim3(p.num_wg), dim3(kBlockWaves * 64), 0, st, p);
   return check_launch("vasc_pooled_softmax");
 }
 

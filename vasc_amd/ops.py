@@ -80,8 +80,9 @@ def pooled_softmax(pooled_q: torch.Tensor, pooled_k: torch.Tensor, *, scale: flo
     kb = pk.shape[2]
     scale = 1.0 / math.sqrt(D) if scale is None else scale
     prob = torch.empty(B, H, qb, kb, device=pq.device, dtype=torch.float32)
+    ws = torch.empty(_lib.load().vasc_pooled_softmax_workspace_size(B, H, qb, kb), device=pq.device, dtype=torch.uint8)
     _lib.call("vasc_pooled_softmax", pq.data_ptr(), pk.data_ptr(), B, H, qb, kb, D, float(scale),
-              int(bool(round_bf16)), prob.data_ptr(), _stream())
+              int(bool(round_bf16)), prob.data_ptr(), ws.data_ptr(), _stream())
     return prob
 
 
