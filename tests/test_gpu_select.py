@@ -48,6 +48,8 @@ def _assert_lists(out, sel, sink):
 @pytest.mark.parametrize("K,topk,force_last,sink,levels", [
     (130, 32, False, 1, None), (130, 32, True, 1, 4), (7, 0, False, 0, 2), (518, 129, False, 3, 8),
     (2072, 259, False, 10, None), (1, 1, False, 2, None), (31, 31, True, 0, 3), (64, 10, True, 4, 1),
+    (1500, 375, True, 1, None), (4096, 1024, True, 2, None), (4096, 1024, False, 0, 16), (6000, 1500, False, 1, None),
+    (8192, 2048, True, 0, 8), (1000, 999, False, 0, None), (3000, 1, True, 0, None),
 ])
 def test_topk_lists_bit_exact(K, topk, force_last, sink, levels):
     from vasc_amd import ops
@@ -60,6 +62,23 @@ def test_topk_lists_bit_exact(K, topk, force_last, sink, levels):
         sel[..., K - 1] = True
     assert np.array_equal(out["mask"].cpu().numpy().astype(bool), sel)
     _assert_lists(out, sel, sink)
+
+
+@pytest.mark.parametrize("K,period,high", [(4096, 8, True), (4096, 8, False), (2072, 16, True), (600, 4, True)])
+def test_topk_periodic_scores_bit_exact(K, period, high):
+    """Scores whose every period-th block is far above (or below) the rest: a
+    strided sample of the row sees a biased distribution, and the selection
+    must stay exact."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(K + period)
+    logits = rng.standard_normal((1, 2, 9, K))
+    logits[..., ::period] += 6.0 if high else -6.0
+    score = _softmax(logits)
+    for topk in (K // period // 2, K // 4, K - K // period // 2):
+        out = ops.select_blocks(torch.from_numpy(score).cuda(), mode=TOPK, topk=topk, want_mask=True)
+        sel = OS.topk_block_mask(score, 0, topk=topk)
+        assert np.array_equal(out["mask"].cpu().numpy().astype(bool), sel), f"topk={topk}"
+        _assert_lists(out, sel, 0)
 
 
 def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=False, levels=None):
@@ -111,6 +130,7 @@ def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=
 
 @pytest.mark.parametrize("K,Q,force_last,peak,levels", [
     (130, 65, True, 1.0, None), (7, 3, False, 3.0, None), (518, 40, False, 2.0, 4), (31, 9, True, 5.0, 2),
+    (4096, 9, True, 2.0, None), (3000, 7, False, 1.0, 8),
 ])
 def test_vasc_chain_bit_exact(K, Q, force_last, peak, levels):
     topk = max(int(K * 0.25), 1)

@@ -25,14 +25,16 @@
 //            accumulated in row order;
 //   head     per head: ledger settlement, arrival mean, pair capacity,
 //            admitted debt, the head's partials of the global gate;
-//   select   one wave per row (1-4 rows per wave), the row in LDS by DMA:
-//            priorities as order-preserving keys in place, the c-th largest
-//            key from one adaptive histogram pass plus an exact rank of the
-//            threshold bin, compaction to the ascending list, pair counts;
+//   select   one row per wave (K <= 1024) or per workgroup, the row in
+//            registers: priorities as order-preserving keys, a sampled
+//            histogram bracketing the c-th largest, the exact threshold
+//            among the bracketed candidates, compaction to the ascending
+//            list staged in LDS, pair counts;
 //   service  QK-admission service from the pair counts.
-// Top-K mode runs the select launch alone. Every pass over a row is a short
-// rolled loop over LDS, so the code stays small for any K.
+// Top-K mode runs the select launch alone.
 #pragma clang fp contract(off)
+
+#include <type_traits>
 
 #include "common.h"
 
@@ -297,25 +299,33 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
 }
 
 // ------------------------------------------------------------------ select
-// The row's keys sit in LDS, key of element k at buf[off + k]; lane l
-// visits LDS elements e = 256 it + 4 l + j (j = 0..3) with one 16-byte read.
-// Slots outside the row (e < off, e >= off + K) hold key 0, which no real
-// value maps to, so the passes below need no range checks: every threshold
-// they compare against is >= 1. Loops go `for (e = 4 lane; e < n4; e += 256)`
-// with n4 = off + K.
+// One wave per row with the row's keys in registers: lane l holds elements
+// k = 256 i + 4 l + j (i < EPT / 4, j < 4), so each 16-byte load of a step
+// is coalesced; key 0 (which no real value maps to) past the row end. Per
+// row:
+//   keys     order-preserving keys of the score (Top-K) or of the priority
+//            (VASC) and the row's key range;
+//   bracket  a 256-bin histogram of every 8th key over that range gives
+//            lo <= hm1 with, very likely, fewer than c keys above hm1 and at
+//            least c keys >= lo (sample ranks c S / K -+ 3 sigma + 1);
+//   rank     histogram levels over the keys in [lo, hm1] (the whole range
+//            when the bracket misses) find the c-th largest key exactly;
+//   compact  the kept indices in ascending order, ties at the threshold
+//            going to the lower index.
+typedef uint32_t u32x4u __attribute__((ext_vector_type(4), aligned(4)));
+typedef float floatx4u __attribute__((ext_vector_type(4), aligned(8)));
 
 // Wave-uniform min and max of the keys in [lo, hi).
-__device__ void range_minmax(const uint32_t *buf, int n4, int lane, uint64_t lo, uint64_t hi, uint32_t &kmin,
-                             uint32_t &kmax) {
+template <int EPT>
+__device__ __forceinline__ void keys_minmax(const uint32_t (&key)[EPT], uint32_t lo, uint64_t hi, uint32_t &kmin,
+                                            uint32_t &kmax) {
   uint32_t mn = 0xffffffffu, mx = 0u;
-  for (int e = 4 * lane; e < n4; e += 256) {
-    const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool in = x[j] >= lo && x[j] < hi;
-      mn = in && x[j] < mn ? x[j] : mn;
-      mx = in && x[j] > mx ? x[j] : mx;
-    }
+  for (int j = 0; j < EPT; ++j) {
+    const bool in = key[j] >= lo && static_cast<uint64_t>(key[j]) < hi;
+    mn = in && key[j] < mn ? key[j] : mn;
+    mx = in && key[j] > mx ? key[j] : mx;
+    if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
@@ -327,97 +337,120 @@ __device__ void range_minmax(const uint32_t *buf, int n4, int lane, uint64_t lo,
   kmax = __builtin_amdgcn_readfirstlane(mx);
 }
 
-// The c-th largest key of the row (1 <= c < K). Each level histograms the
-// keys of the current range [kmin, kmax] into 256 bins of width 2^s (LDS
-// atomics; keys above the range are counted in `above`) and a suffix scan
-// picks the bin holding the c-th largest key. The search ends when that bin
-// is consumed whole (every key >= its lower edge is kept), when its keys are
-// all equal, or when it holds at most 64 keys: those are compacted one per
-// lane and ranked exactly with readlane compares. Otherwise the bin's own
-// [min, max] becomes the next level's range (each level shrinks the range
-// by at least 2^8). Returns T; need = how many keys equal to T to keep in
-// index order (INT_MAX: all of them) and eqT = how many keys equal T.
-__device__ uint32_t find_threshold(const uint32_t *buf, int n4, int lane, uint32_t kmin, uint32_t kmax, int c,
-                                   int n, int &need, int &eqT, uint32_t *hist) {
-  int above = 0;   // keys > kmax (outside the current range, all kept)
-  int inr = n;     // keys inside [kmin, kmax]
+// 256-bin histogram (this wave's `hist`) of the keys in [kmin, kmin + 256 <<
+// sh), read back as four bins per lane plus the inclusive suffix sum over
+// lanes (keys in bins >= 4 lane).
+__device__ __forceinline__ int hist_suffix(const uint32_t *hist, int lane, u32x4 &h) {
+  h = *reinterpret_cast<const u32x4 *>(hist + 4 * lane);
+  int suf = static_cast<int>(h[0] + h[1] + h[2] + h[3]);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_down(suf, o);
+    if (lane + o < 64) suf += t;
+  }
+  return suf;
+}
+
+// Bin holding the r-th largest histogram entry (1 <= r <= total), or -1.
+__device__ __forceinline__ int rank_bin(const u32x4 &h, int suf, int lane, int r) {
+  int found = -1, above = suf;  // above: entries in bins >= the current one
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int next = above - static_cast<int>(h[b]);
+    if (above >= r && next < r) found = 4 * lane + b;
+    above = next;
+  }
+  const uint64_t bal = __ballot(found >= 0);
+  return bal ? __builtin_amdgcn_readlane(found, __builtin_ctzll(bal)) : -1;
+}
+
+// The c-th largest key (c >= 1) counting from the top of [kmin, kmax];
+// keys above kmax are counted first. Each level histograms the keys of the
+// current range into 256 bins of width 2^sh and takes the bin holding the
+// rank; the search ends when that bin is kept whole, when its keys are all
+// equal, or when it holds at most 64 keys (ranked exactly with readlane
+// compares); otherwise the bin's own [min, max] is the next range. Returns
+// false (nothing written) when the c-th largest key is not inside the
+// first range. T: the threshold; need: how many keys equal to T to keep in
+// index order (INT_MAX: all); eqT: how many keys equal T.
+template <int EPT>
+__device__ bool rank_keys(const uint32_t (&key)[EPT], int lane, uint32_t kmin, uint32_t kmax, int c, uint32_t *hist,
+                          uint32_t *sbuf, uint32_t &T, int &need, int &eqT) {
+  int above = 0;
 #pragma unroll 1
   for (int level = 0;; ++level) {
-    if (kmin == kmax) {  // every key of the range is equal: keep the first need of them
-      need = c - above;
-      eqT = inr;
-      return kmax;
-    }
     const uint32_t range = kmax - kmin;
-    const int sh = 32 - __clz(range) > 8 ? 32 - __clz(range) - 8 : 0;  // (range >> sh) < 256
+    const int sh = 32 - __clz(range) > 8 ? 32 - __clz(range) - 8 : 0;
     *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
     wave_sync();
-    if (level == 0) {  // the whole row: every key but the 0 slots is in range
-      for (int e = 4 * lane; e < n4; e += 256) {
-        const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
+    int over = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (x[j] != 0u) atomicAdd(&hist[(x[j] - kmin) >> sh], 1u);
-      }
-    } else {
-      for (int e = 4 * lane; e < n4; e += 256) {
-        const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (x[j] >= kmin && x[j] <= kmax) atomicAdd(&hist[(x[j] - kmin) >> sh], 1u);
-      }
+    for (int j = 0; j < EPT; ++j) {
+      // branch-free: keys outside the range count into the lane's trash bin
+      const uint32_t x = key[j];
+      const bool in = x >= kmin && x <= kmax;
+      atomicAdd(&hist[in ? (x - kmin) >> sh : 256u + lane], 1u);
+      over += x > kmax;
+      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // keeps few element masks live
     }
     wave_sync();
-    const u32x4 h = *reinterpret_cast<const u32x4 *>(hist + 4 * lane);
-    const int v = static_cast<int>(h[0] + h[1] + h[2] + h[3]);
-    int suf = v;  // keys in bins 4*lane .. 255 (inclusive suffix)
+    u32x4 h;
+    const int suf = hist_suffix(hist, lane, h);
+    const int inr = __builtin_amdgcn_readfirstlane(suf);
+    if (level == 0) {
+      above = __builtin_amdgcn_readfirstlane(wave_sum_int(over));
+      if (c - above < 1 || c - above > inr) return false;
+    }
+    if (range == 0) {  // every key of the range is equal
+      T = kmin;
+      need = c - above;
+      eqT = inr;
+      return true;
+    }
+    const int need_r = c - above;
+    const int bin = rank_bin(h, suf, lane, need_r);
+    // keys in bins above `bin` and in `bin` itself
+    int abv = 0, inb = 0;
+    {
+      int a = suf;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_down(suf, o);
-      if (lane + o < 64) suf += t;
-    }
-    const int need_r = c - above;  // keys still to find inside the range
-    const int L = 63 - __clzll(static_cast<long long>(__ballot(suf >= need_r)));
-    int bin = 0, abv = 0, inb = 0;
-    if (lane == L) {
-      abv = suf - v;
-      for (int bb = 3; bb >= 0; --bb) {
-        if (abv + static_cast<int>(h[bb]) >= need_r) {
-          bin = 4 * L + bb;
-          inb = static_cast<int>(h[bb]);
-          break;
+      for (int b = 0; b < 4; ++b) {
+        if (4 * lane + b == bin) {
+          inb = static_cast<int>(h[b]);
+          abv = a - inb;
         }
-        abv += static_cast<int>(h[bb]);
+        a -= static_cast<int>(h[b]);
       }
+      const uint64_t bal = __ballot(bin >= 4 * lane && bin < 4 * lane + 4);
+      const int L = __builtin_ctzll(bal);
+      abv = __builtin_amdgcn_readlane(abv, L);
+      inb = __builtin_amdgcn_readlane(inb, L);
     }
-    bin = __builtin_amdgcn_readlane(bin, L);
-    abv = __builtin_amdgcn_readlane(abv, L);
-    inb = __builtin_amdgcn_readlane(inb, L);
     above += abv;
     const int need_b = c - above;  // 1 <= need_b <= inb
     const uint32_t lowT = kmin + (static_cast<uint32_t>(bin) << sh);
     const uint64_t highT = bin == 255 ? static_cast<uint64_t>(kmax) + 1u
                                       : static_cast<uint64_t>(kmin) + (static_cast<uint64_t>(bin + 1) << sh);
     if (need_b == inb) {
+      T = lowT;
       need = 0x7fffffff;
       eqT = 0;
-      return lowT;
+      return true;
     }
     if (inb <= 64) {
-      // The bin's keys, one per lane (order irrelevant), then exact ranks.
+      // the bin's keys, one per lane (order irrelevant), then exact ranks
       int n = 0;
-      for (int e = 4 * lane; e < n4; e += 256) {
-        const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool in = x[j] >= lowT && static_cast<uint64_t>(x[j]) < highT;
-          const uint64_t bal = __ballot(in);
-          if (in) hist[n + __popcll(bal & lanemask_lt())] = x[j];
-          n += __popcll(bal);
-        }
+      for (int j = 0; j < EPT; ++j) {
+        // branch-free: lanes without a bin key write their trash slot
+        const bool in = key[j] >= lowT && static_cast<uint64_t>(key[j]) < highT;
+        const uint64_t bal = __ballot(in);
+        sbuf[in ? n + __popcll(bal & lanemask_lt()) : 64 + lane] = key[j];
+        n += __popcll(bal);
+        if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
       wave_sync();
-      const uint32_t mine = lane < inb ? hist[lane] : 0u;
+      const uint32_t mine = lane < inb ? sbuf[lane] : 0u;
       int gt = 0, eq = 0;
       for (int jj = 0; jj < inb; ++jj) {
         const uint32_t x = __builtin_amdgcn_readlane(mine, jj);
@@ -428,25 +461,98 @@ __device__ uint32_t find_threshold(const uint32_t *buf, int n4, int lane, uint32
       const int Lt = __builtin_ctzll(__ballot(isT));
       need = need_b - __builtin_amdgcn_readlane(gt, Lt);
       eqT = __builtin_amdgcn_readlane(eq, Lt);
-      return __builtin_amdgcn_readlane(mine, Lt);
+      T = __builtin_amdgcn_readlane(mine, Lt);
+      return true;
     }
-    inr = inb;
-    range_minmax(buf, n4, lane, lowT, highT, kmin, kmax);  // next level: the bin's own range
+    keys_minmax(key, lowT, highT, kmin, kmax);  // next level: the bin's own range
   }
 }
 
-// One wave per row, rows_per_wave consecutive rows per wave, kWaves waves per
-// workgroup (all rows of one head). LDS: the waves' row buffers, their
-// histograms, then the workgroup's pair counts (VASC).
-template <bool kVasc>
-__global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int bufn, int rows_per_wave) {
+// Sample-rank margin: 3 standard deviations of the count of S samples above
+// a fraction f of the row, plus one.
+__device__ __forceinline__ int sample_margin(int S, int c, int K) {
+  const float f = static_cast<float>(c) / static_cast<float>(K);
+  return static_cast<int>(3.f * __builtin_sqrtf(static_cast<float>(S) * f * (1.f - f))) + 1;
+}
+
+// Ascending compaction of the kept keys: element (lane, j) of a 256-element
+// step follows every element of lower lanes and its own j' < j; ties at T
+// are kept in index order up to need when split. kMask: writes the 0/1
+// mask (every element of the row) instead of the index list and pair
+// counts. Returns the number kept.
+template <bool kVasc, bool kMask, int EPT>
+__device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane, uint32_t T, int need, bool split,
+                                           bool none, uint32_t tsel, int64_t width, int32_t *irow,
+                                           uint32_t *pair_cnt, uint8_t *mrow) {
+  int run_sel = 0, run_eq = 0;
+#pragma unroll
+  for (int i = 0; i < EPT / 4; ++i) {
+    bool sel[4];
+    if (split) {
+      bool eq[4];
+      uint64_t beq[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        eq[j] = key[4 * i + j] == T;
+        beq[j] = __ballot(eq[j]);
+      }
+      int eq_rank = run_eq;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) eq_rank += __popcll(beq[j] & lanemask_lt());
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sel[j] = key[4 * i + j] > T || (eq[j] && eq_rank < need);
+        eq_rank += eq[j] ? 1 : 0;
+        run_eq += __popcll(beq[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sel[j] = !none && key[4 * i + j] >= tsel;
+    }
+    const int kk = 256 * i + 4 * lane;
+    if (kMask) {
+      // key 0 marks slots past the row end
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (key[4 * i + j] != 0u) mrow[kk + j] = sel[j] ? 1 : 0;
+    } else {
+      uint64_t bsel[4];
+      int pos = run_sel;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bsel[j] = __ballot(sel[j]);
+        pos += __popcll(bsel[j] & lanemask_lt());
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (sel[j]) {
+          if (pos < width) irow[pos] = kk + j;
+          if (kVasc) atomicAdd(&pair_cnt[(kk + j) >> 1], 1u);
+          ++pos;
+        }
+        run_sel += __popcll(bsel[j]);
+      }
+    }
+  }
+  return run_sel;
+}
+
+// per wave: histogram (256 bins + 64 per-lane trash bins), small-bin keys
+// (64 + 64 per-lane trash slots)
+constexpr int kWaveLds = 256 + 64 + 128;
+
+// kWaves waves per workgroup, rows_per_wave consecutive rows per wave (all
+// rows of one head); LDS: the waves' histograms and small-bin buffers, then
+// the workgroup's pair counts (VASC).
+template <bool kVasc, int EPT>
+__global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int rows_per_wave) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
+  const int tid = threadIdx.x, lane0 = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint32_t *hist = lds + w * kWaveLds;
+  uint32_t *sbuf = hist + 256 + 64;
+  uint32_t *pair_cnt = lds + kWaves * kWaveLds;
   const int64_t bh = blockIdx.y;
-  uint32_t *buf = lds + w * bufn;
-  uint32_t *hist = lds + kWaves * bufn + w * 256;
-  uint32_t *pair_cnt = lds + kWaves * (bufn + 256);
   const int K = static_cast<int>(p.K);
   int gate = 0;
   if (kVasc) {
@@ -455,16 +561,46 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int b
     gate = service_gate(p);
   }
   const float2 *ia = kVasc ? p.ia + bh * p.P : nullptr;
+  const uint32_t top = order_key(kFltMax);
+  // the forced value (protected / forced last blocks) is left out of the
+  // bracket histogram's range, which it would otherwise stretch
+  const uint32_t forced = kVasc ? top : 0xffffffffu;
 
   for (int rr = 0; rr < rows_per_wave; ++rr) {
     const int64_t q = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * rows_per_wave + rr;
     if (q >= p.Q) break;
     const int64_t row = bh * p.Q + q;
     const float *srow = p.score + row * p.K;
-    const int off = dma_row(srow, K, buf, lane);
-    wait_dma();
+    // An opaque copy of the lane index: per-element indices and masks are
+    // recomputed in every row instead of being hoisted out of the row loop
+    // (64-bit masks for every element would spill).
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
 
-    // Keys in place: order_key of the score (Top-K) or of the priority (VASC).
+    // ---- load and keys. Whether a 256-element step lies wholly inside the
+    // row is wave-uniform, so the branches are scalar and every load of the
+    // row is issued before the first wait; in the step holding the row end
+    // each element loads from a clamped (in-bounds) index.
+    uint32_t key[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT / 4; ++i) {
+      const int kk = 256 * i + 4 * lane;
+      if (256 * (i + 1) <= K) {
+        const u32x4u x = *reinterpret_cast<const u32x4u *>(srow + kk);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) key[4 * i + j] = x[j];
+      } else if (256 * i < K) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = kk + j;
+          const uint32_t v = __float_as_uint(srow[k < K ? k : K - 1]);
+          key[4 * i + j] = k < K ? v : 0u;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) key[4 * i + j] = 0u;
+      }
+    }
     int c;
     float total = 0.f, scale = 0.f;
     uint32_t last = 0;
@@ -476,117 +612,132 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int b
     } else {
       c = p.topk < 1 ? 1 : p.topk;
       c = c > K ? K : c;
-      last = order_key(__uint_as_float(buf[off + K - 1]));
+      last = order_key(srow[K - 1]);
     }
-    const uint32_t top = order_key(kFltMax);
-    uint32_t kmin = 0xffffffffu, kmax = 0u;
+    uint32_t kmin = 0xffffffffu, kmax = 0u, kmaxh = 0u;
     int beat = 0;
-    const int n4 = off + K;
-    // The first and last 16-byte groups may hold slots outside the row: they
-    // become key 0.
-    for (int e = 4 * lane; e < n4; e += 256) {
-      u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = e + j - off;
-        if (k < 0 || k >= K) {
-          x[j] = 0u;
+    // Steps wholly before the last element need no per-element masks; only
+    // the step holding the last element (K - 1) checks k < K and k == K - 1
+    // (which step that is, is wave-uniform).
+    auto transform = [&](const int i, auto edge_c) {
+      constexpr bool kEdge = decltype(edge_c)::value;
+      const int kk = 256 * i + 4 * lane;
+      // (innovation, admitted debt) of the step's two pairs kk/2, kk/2 + 1
+      // (pair indices clamped into [0, P) in the step holding the row end)
+      floatx4 pa = {0.f, 0.f, 0.f, 0.f};
+      if (kVasc) {
+        if (!kEdge) {
+          const floatx4u x = *reinterpret_cast<const floatx4u *>(ia + (kk >> 1));
+          pa = floatx4{x[0], x[1], x[2], x[3]};
         } else {
-          uint32_t key;
-          if (kVasc) {
-            const float2 pa = ia[k >> 1];
-            float A = 0.f;
-            if (total > 0.f) A = clamp01((clean_score(__uint_as_float(x[j])) * pa.x) * scale);
-            key = order_key(gate ? A + pa.y : A);
-            if (p.protected_mask && p.protected_mask[row * p.K + k]) key = top;
-            if (p.force_last && k == K - 1) key = top;
-          } else {
-            key = order_key(__uint_as_float(x[j]));
-            beat += (key > last) || (key == last && k < K - 1);
-            if (p.force_last && k == K - 1) key = 0xffffffffu;
-          }
-          x[j] = key;
-          kmin = key < kmin ? key : kmin;
-          kmax = key > kmax ? key : kmax;
+          const int P = (K + 1) >> 1, p0 = kk >> 1;
+          const float2 x0 = ia[p0 < P ? p0 : P - 1], x1 = ia[p0 + 1 < P ? p0 + 1 : P - 1];
+          pa = floatx4{x0.x, x0.y, x1.x, x1.y};
         }
       }
-      *reinterpret_cast<u32x4 *>(buf + e) = x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = kk + j;
+        const bool ok = !kEdge || k < K;
+        const bool is_last = kEdge && k == K - 1;
+        const float sv = __uint_as_float(key[4 * i + j]);
+        uint32_t kj;
+        if (kVasc) {
+          const float pin = pa[2 * (j >> 1)], pad = pa[2 * (j >> 1) + 1];
+          const float A = total > 0.f ? clamp01((clean_score(sv) * pin) * scale) : 0.f;
+          kj = order_key(gate ? A + pad : A);
+          if (p.protected_mask) kj = ok && p.protected_mask[row * p.K + k] ? top : kj;
+          kj = p.force_last && is_last ? top : kj;
+        } else {
+          kj = order_key(sv);
+          beat += ok && ((kj > last) || (kj == last && !is_last)) ? 1 : 0;
+          kj = p.force_last && is_last ? 0xffffffffu : kj;
+        }
+        kj = ok ? kj : 0u;
+        kmin = ok && kj < kmin ? kj : kmin;
+        kmax = kj > kmax ? kj : kmax;
+        kmaxh = kj != forced && kj > kmaxh ? kj : kmaxh;
+        key[4 * i + j] = kj;
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < EPT / 4; ++i) {
+      if (256 * (i + 1) < K)
+        transform(i, std::false_type{});
+      else if (256 * i < K)
+        transform(i, std::true_type{});
     }
-    if (!kVasc && p.force_last && c < K) c += wave_sum_int(beat) >= c ? 1 : 0;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
-      const uint32_t a = __shfl_xor(kmin, o), b = __shfl_xor(kmax, o);
+      const uint32_t a = __shfl_xor(kmin, o), b = __shfl_xor(kmax, o), d = __shfl_xor(kmaxh, o);
       kmin = a < kmin ? a : kmin;
       kmax = b > kmax ? b : kmax;
+      kmaxh = d > kmaxh ? d : kmaxh;
     }
     kmin = __builtin_amdgcn_readfirstlane(kmin);
     kmax = __builtin_amdgcn_readfirstlane(kmax);
+    kmaxh = __builtin_amdgcn_readfirstlane(kmaxh);
+    if (kmaxh < kmin) kmaxh = kmax;  // every key is forced
+    if (!kVasc && p.force_last && c < K) c += wave_sum_int(beat) >= c ? 1 : 0;
     c = c < 0 ? 0 : (c > K ? K : c);
+    c = __builtin_amdgcn_readfirstlane(c);  // wave-uniform: keeps the control flow below scalar
     const bool all = c >= K, none = c == 0;
+
+    // ---- threshold: keys > T kept, keys == T kept in index order up to need
     uint32_t T = 1u;
     int need = 0x7fffffff, eqT = 0;
-    if (none) T = 0xffffffffu;  // with `none` nothing is selected below
-    if (!all && !none) T = find_threshold(buf, n4, lane, kmin, kmax, c, K, need, eqT, hist);
+    if (none) T = 0xffffffffu;
+    if (!all && !none) {
+      // bracket from every 8th key (steps i even, j == 0)
+      const uint32_t range = kmaxh - kmin;
+      const int sh = 32 - __clz(range) > 8 ? 32 - __clz(range) - 8 : 0;
+      *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
+      wave_sync();
+#pragma unroll
+      for (int i = 0; i < EPT / 4; i += 2) {
+        const uint32_t x = key[4 * i];
+        atomicAdd(&hist[x != 0u && x <= kmaxh ? (x - kmin) >> sh : 256u + lane], 1u);
+      }
+      wave_sync();
+      u32x4 h;
+      const int suf = hist_suffix(hist, lane, h);
+      const int S = __builtin_amdgcn_readfirstlane(suf);
+      const int rs = static_cast<int>(static_cast<int64_t>(c) * S / K);
+      const int m = sample_margin(S, c, K);
+      const int bin_hi = rs - m >= 1 ? rank_bin(h, suf, lane, rs - m) : -1;
+      const int bin_lo = rs + m <= S ? rank_bin(h, suf, lane, rs + m) : -1;
+      uint32_t hm1 = kmax, lo = kmin;  // keys > hm1 kept outright; candidates in [lo, hm1]
+      if (bin_hi >= 0 && bin_hi < 255) {
+        const uint64_t e = static_cast<uint64_t>(kmin) + (static_cast<uint64_t>(bin_hi + 1) << sh);
+        if (e <= kmaxh) hm1 = static_cast<uint32_t>(e - 1);
+      }
+      if (bin_lo >= 0) lo = kmin + (static_cast<uint32_t>(bin_lo) << sh);
+      if (lo > hm1) lo = kmin;
+      if (!rank_keys(key, lane, lo, hm1, c, hist, sbuf, T, need, eqT))
+        rank_keys(key, lane, kmin, kmax, c, hist, sbuf, T, need, eqT);  // missed bracket: the whole range
+    }
     const bool split = !all && !none && need < eqT;
-    const uint32_t tsel = all ? 1u : T;  // keys >= tsel are kept (no split); key 0 is never a row element
+    const uint32_t tsel = all ? 1u : T;  // keys >= tsel are kept (no split)
 
-    // Ascending compaction: element (lane, j) of a 256-element step follows
-    // every element of lower lanes and its own j' < j.
+    // ---- ascending compaction (indices and pair counts), then the optional
+    // mask and priority outputs in passes of their own
     int32_t *irow = p.index_out + row * p.width;
-    int run_sel = 0, run_eq = 0;
-    for (int e = 4 * lane; e < n4; e += 256) {
-      const u32x4 x = *reinterpret_cast<const u32x4 *>(buf + e);
-      bool eq[4], sel[4];
-      uint64_t bsel[4];
-      if (split) {
-        uint64_t beq[4];
+    asm volatile("" : "+v"(lane));  // element indices recomputed here, not kept from the loads
+    const int run_sel = compact_row<kVasc, false, EPT>(key, lane, T, need, split, none, tsel, p.width, irow,
+                                                      pair_cnt, nullptr);
+    if (p.mask_out)
+      compact_row<kVasc, true, EPT>(key, lane, T, need, split, none, tsel, p.width, nullptr, nullptr,
+                                    p.mask_out + row * p.K);
+    if (kVasc && p.priority_out) {
+#pragma unroll
+      for (int i = 0; i < EPT / 4; ++i) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          eq[j] = x[j] == T;
-          beq[j] = __ballot(eq[j]);
-        }
-        int eq_rank = run_eq;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) eq_rank += __popcll(beq[j] & lanemask_lt());
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          sel[j] = x[j] > T || (eq[j] && eq_rank < need);
-          eq_rank += eq[j] ? 1 : 0;
-          run_eq += __popcll(beq[j]);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sel[j] = !none && x[j] >= tsel;
-      }
-      int pos = run_sel;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bsel[j] = __ballot(sel[j]);
-        pos += __popcll(bsel[j] & lanemask_lt());
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = e + j - off;
-        if (sel[j]) {
-          if (pos < p.width) irow[pos] = k;
-          if (kVasc) atomicAdd(&pair_cnt[k >> 1], 1u);
-          ++pos;
-        }
-        run_sel += __popcll(bsel[j]);
-      }
-      if (p.mask_out || (kVasc && p.priority_out)) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int k = e + j - off;
-          if (k >= 0 && k < K) {
-            if (p.mask_out) p.mask_out[row * p.K + k] = sel[j] ? 1 : 0;
-            if (kVasc && p.priority_out) p.priority_out[row * p.K + k] = __uint_as_float(x[j] & 0x7fffffffu);
-          }
+          const int k = 256 * i + 4 * lane + j;
+          if (k < K) p.priority_out[row * p.K + k] = __uint_as_float(key[4 * i + j] & 0x7fffffffu);
         }
       }
     }
-    // Lanes leave the loop at different steps; lane 0 saw every step.
-    run_sel = __builtin_amdgcn_readlane(run_sel, 0);
     for (int i = lane; i < p.sink && run_sel + i < p.width; i += 64) irow[run_sel + i] = static_cast<int32_t>(p.K + i);
     if (lane == 0) p.count_out[row] = run_sel + p.sink;
   }
@@ -648,6 +799,43 @@ int reserve_lds(const void *kern, size_t lds) {
   return VASC_OK;
 }
 
+template <bool kVasc, int EPT>
+int launch_select_cfg(const SelectParams &p, hipStream_t s) {
+  // Rows per wave: enough waves to give every SIMD several (1..4 rows);
+  // VASC accumulates pair counts per workgroup, so more rows per workgroup
+  // keep the global count atomics down.
+  const int64_t rows = p.BH * p.Q;
+  const int rpw = static_cast<int>(rows >= 4 * 8192 ? 4 : (rows >= 2 * 8192 ? 2 : 1));
+  const size_t lds = (static_cast<size_t>(kWaves) * kWaveLds + (kVasc ? static_cast<size_t>(p.P) : 0)) * 4;
+  const void *kern = reinterpret_cast<const void *>(select_kernel<kVasc, EPT>);
+  int rc;
+  if ((rc = reserve_lds(kern, lds))) return rc;
+  const dim3 grid(static_cast<unsigned>(cdiv(p.Q, static_cast<int64_t>(kWaves) * rpw)), static_cast<unsigned>(p.BH));
+  hipLaunchKernelGGL((select_kernel<kVasc, EPT>), grid, dim3(256), lds, s, p, rpw);
+  return check_launch("vasc_select_blocks/select");
+}
+
+// Keys per lane: the row rounded up to whole 256-element steps.
+template <bool kVasc>
+int launch_select_mode(const SelectParams &p, hipStream_t s) {
+  const int64_t K = p.K;
+  if (K <= 256) return launch_select_cfg<kVasc, 4>(p, s);
+  if (K <= 512) return launch_select_cfg<kVasc, 8>(p, s);
+  if (K <= 768) return launch_select_cfg<kVasc, 12>(p, s);
+  if (K <= 1024) return launch_select_cfg<kVasc, 16>(p, s);
+  if (K <= 1536) return launch_select_cfg<kVasc, 24>(p, s);
+  if (K <= 2048) return launch_select_cfg<kVasc, 32>(p, s);
+  if (K <= 2304) return launch_select_cfg<kVasc, 36>(p, s);
+  if (K <= 3072) return launch_select_cfg<kVasc, 48>(p, s);
+  if (K <= 4096) return launch_select_cfg<kVasc, 64>(p, s);
+  if (K <= 6144) return launch_select_cfg<kVasc, 96>(p, s);
+  return launch_select_cfg<kVasc, 128>(p, s);
+}
+
+int launch_select(const SelectParams &p, bool vasc, hipStream_t s) {
+  return vasc ? launch_select_mode<true>(p, s) : launch_select_mode<false>(p, s);
+}
+
 int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
   const int64_t bufn = row_buf_elems(p.K);
   int rc;
@@ -665,19 +853,7 @@ int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
                        dim3(256), 0, s, p);
     if ((rc = check_launch("vasc_select_blocks/head"))) return rc;
   }
-  // Rows per wave: enough waves to give every SIMD about four (1..4 rows).
-  const int64_t rows = p.BH * p.Q;
-  const int rpw = static_cast<int>(rows >= 4 * 4096 ? 4 : (rows >= 2 * 4096 ? 2 : 1));
-  const size_t lds = static_cast<size_t>(kWaves) * (bufn + 256) * 4 + (vasc ? static_cast<size_t>(p.P) * 4 : 0);
-  const void *kern = vasc ? reinterpret_cast<const void *>(select_kernel<true>)
-                          : reinterpret_cast<const void *>(select_kernel<false>);
-  if ((rc = reserve_lds(kern, lds))) return rc;
-  const dim3 grid(static_cast<unsigned>(cdiv(p.Q, static_cast<int64_t>(kWaves) * rpw)), static_cast<unsigned>(p.BH));
-  if (vasc)
-    hipLaunchKernelGGL(select_kernel<true>, grid, dim3(256), lds, s, p, static_cast<int>(bufn), rpw);
-  else
-    hipLaunchKernelGGL(select_kernel<false>, grid, dim3(256), lds, s, p, static_cast<int>(bufn), rpw);
-  if ((rc = check_launch("vasc_select_blocks/select"))) return rc;
+  if ((rc = launch_select(p, vasc, s))) return rc;
   if (vasc) {
     hipLaunchKernelGGL(service_kernel, dim3(static_cast<unsigned>(cdiv(p.BH * p.P, 256))), dim3(256), 0, s, p);
     if ((rc = check_launch("vasc_select_blocks/service"))) return rc;
