@@ -81,6 +81,28 @@ def test_topk_periodic_scores_bit_exact(K, period, high):
         _assert_lists(out, sel, 0)
 
 
+@pytest.mark.parametrize("K", [130, 2072, 4096])
+def test_topk_signed_scores_bit_exact(K):
+    """Scores that are not probabilities: negatives, -0.0 next to +0.0, a NaN
+    and infinities take the full order-key path and keep the oracle's order
+    (NaN largest, -0 == +0, ties to the lower index)."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(K)
+    score = rng.standard_normal((1, 2, 5, K)).astype(np.float32)
+    score[0, 0, 0, :8] = [-0.0, 0.0, -0.0, np.nan, np.inf, -np.inf, 0.0, -0.0]
+    score[0, 1, 2, ::3] = np.float32(-0.0)
+    score[0, 1, 3] = np.abs(score[0, 1, 3])  # one all-positive row between signed ones
+    for topk in (1, K // 4, K - 1):
+        for force_last in (False, True):
+            out = ops.select_blocks(torch.from_numpy(score).cuda(), mode=TOPK, topk=topk, force_last=force_last,
+                                    want_mask=True)
+            sel = OS.topk_block_mask(score, 0, topk=topk)
+            if force_last:
+                sel[..., K - 1] = True
+            assert np.array_equal(out["mask"].cpu().numpy().astype(bool), sel), f"topk={topk} force_last={force_last}"
+            _assert_lists(out, sel, 0)
+
+
 def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=False, levels=None):
     from vasc_amd import ops
     rng = np.random.default_rng(seed)

@@ -76,6 +76,12 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return (uint64_t(1) << lane_id()) - 1;
 }
 
+// Number of set bits of a wave mask below this lane (v_mbcnt_lo/hi).
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
+
 // Canonical 64-lane xor butterfly of float64 lane sums (offsets 32..1).
 __device__ __forceinline__ double wave_butterfly(double s) {
 #pragma unroll

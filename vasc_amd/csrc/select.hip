@@ -360,7 +360,7 @@ __device__ __forceinline__ int rank_bin(const u32x4 &h, int suf, int lane, int r
     if (above >= r && next < r) found = 4 * lane + b;
     above = next;
   }
-  const uint64_t bal = __ballot(found >= 0);
+  const uint64_t bal = __builtin_amdgcn_ballot_w64(found >= 0);
   return bal ? __builtin_amdgcn_readlane(found, __builtin_ctzll(bal)) : -1;
 }
 
@@ -421,7 +421,7 @@ __device__ bool rank_keys(const uint32_t (&key)[EPT], int lane, uint32_t kmin, u
         }
         a -= static_cast<int>(h[b]);
       }
-      const uint64_t bal = __ballot(bin >= 4 * lane && bin < 4 * lane + 4);
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(bin >= 4 * lane && bin < 4 * lane + 4);
       const int L = __builtin_ctzll(bal);
       abv = __builtin_amdgcn_readlane(abv, L);
       inb = __builtin_amdgcn_readlane(inb, L);
@@ -444,8 +444,8 @@ __device__ bool rank_keys(const uint32_t (&key)[EPT], int lane, uint32_t kmin, u
       for (int j = 0; j < EPT; ++j) {
         // branch-free: lanes without a bin key write their trash slot
         const bool in = key[j] >= lowT && static_cast<uint64_t>(key[j]) < highT;
-        const uint64_t bal = __ballot(in);
-        sbuf[in ? n + __popcll(bal & lanemask_lt()) : 64 + lane] = key[j];
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+        sbuf[in ? n + lanes_below(bal) : 64 + lane] = key[j];
         n += __popcll(bal);
         if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
@@ -458,13 +458,112 @@ __device__ bool rank_keys(const uint32_t (&key)[EPT], int lane, uint32_t kmin, u
         eq += x == mine;
       }
       const bool isT = lane < inb && gt < need_b && need_b <= gt + eq;
-      const int Lt = __builtin_ctzll(__ballot(isT));
+      const int Lt = __builtin_ctzll(__builtin_amdgcn_ballot_w64(isT));
       need = need_b - __builtin_amdgcn_readlane(gt, Lt);
       eqT = __builtin_amdgcn_readlane(eq, Lt);
       T = __builtin_amdgcn_readlane(mine, Lt);
       return true;
     }
     keys_minmax(key, lowT, highT, kmin, kmax);  // next level: the bin's own range
+  }
+}
+
+// The c-th largest key (c >= 1) of the candidate keys in LDS, all inside
+// [kmin, kmax]: lane l holds cnt of them at seg[0 .. cnt) (its own segment,
+// maxcnt the wave's largest cnt). The histogram levels of rank_keys over
+// the candidates; same outputs as rank_keys.
+__device__ void rank_segs(const uint32_t *seg, int cnt, int maxcnt, int lane, uint32_t kmin, uint32_t kmax, int c,
+                          uint32_t *hist, uint32_t *sbuf, uint32_t &T, int &need, int &eqT) {
+  int above = 0;
+#pragma unroll 1
+  for (;;) {
+    const uint32_t range = kmax - kmin;
+    const int sh = 32 - __clz(range) > 8 ? 32 - __clz(range) - 8 : 0;
+    *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
+    wave_sync();
+    for (int r = 0; r < maxcnt; ++r) {
+      const uint32_t x = r < cnt ? seg[r] : 0u;  // key 0: never inside the range
+      const bool in = x >= kmin && x <= kmax;
+      atomicAdd(&hist[in ? (x - kmin) >> sh : 256u + lane], 1u);
+    }
+    wave_sync();
+    u32x4 h;
+    const int suf = hist_suffix(hist, lane, h);
+    const int inr = __builtin_amdgcn_readfirstlane(suf);
+    if (range == 0) {
+      T = kmin;
+      need = c - above;
+      eqT = inr;
+      return;
+    }
+    const int need_r = c - above;
+    const int bin = rank_bin(h, suf, lane, need_r);
+    int abv = 0, inb = 0;
+    {
+      int a = suf;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (4 * lane + b == bin) {
+          inb = static_cast<int>(h[b]);
+          abv = a - inb;
+        }
+        a -= static_cast<int>(h[b]);
+      }
+      const int L = __builtin_ctzll(__builtin_amdgcn_ballot_w64(bin >= 4 * lane && bin < 4 * lane + 4));
+      abv = __builtin_amdgcn_readlane(abv, L);
+      inb = __builtin_amdgcn_readlane(inb, L);
+    }
+    above += abv;
+    const int need_b = c - above;  // 1 <= need_b <= inb
+    const uint32_t lowT = kmin + (static_cast<uint32_t>(bin) << sh);
+    const uint64_t highT = bin == 255 ? static_cast<uint64_t>(kmax) + 1u
+                                      : static_cast<uint64_t>(kmin) + (static_cast<uint64_t>(bin + 1) << sh);
+    if (need_b == inb) {
+      T = lowT;
+      need = 0x7fffffff;
+      eqT = 0;
+      return;
+    }
+    if (inb <= 64) {
+      int m = 0;
+      for (int r = 0; r < maxcnt; ++r) {
+        const uint32_t x = r < cnt ? seg[r] : 0u;
+        const bool in = x >= lowT && static_cast<uint64_t>(x) < highT;
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+        sbuf[in ? m + lanes_below(bal) : 64 + lane] = x;
+        m += __popcll(bal);
+      }
+      wave_sync();
+      const uint32_t mine = lane < inb ? sbuf[lane] : 0u;
+      int gt = 0, eq = 0;
+      for (int jj = 0; jj < inb; ++jj) {
+        const uint32_t x = __builtin_amdgcn_readlane(mine, jj);
+        gt += x > mine;
+        eq += x == mine;
+      }
+      const bool isT = lane < inb && gt < need_b && need_b <= gt + eq;
+      const int Lt = __builtin_ctzll(__builtin_amdgcn_ballot_w64(isT));
+      need = need_b - __builtin_amdgcn_readlane(gt, Lt);
+      eqT = __builtin_amdgcn_readlane(eq, Lt);
+      T = __builtin_amdgcn_readlane(mine, Lt);
+      return;
+    }
+    // next level: the bin's own key range
+    uint32_t mn = 0xffffffffu, mx = 0u;
+    for (int r = 0; r < maxcnt; ++r) {
+      const uint32_t x = r < cnt ? seg[r] : 0u;
+      const bool in = x >= lowT && static_cast<uint64_t>(x) < highT;
+      mn = in && x < mn ? x : mn;
+      mx = in && x > mx ? x : mx;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint32_t a = __shfl_xor(mn, o), b = __shfl_xor(mx, o);
+      mn = a < mn ? a : mn;
+      mx = b > mx ? b : mx;
+    }
+    kmin = __builtin_amdgcn_readfirstlane(mn);
+    kmax = __builtin_amdgcn_readfirstlane(mx);
   }
 }
 
@@ -477,13 +576,15 @@ __device__ __forceinline__ int sample_margin(int S, int c, int K) {
 
 // Ascending compaction of the kept keys: element (lane, j) of a 256-element
 // step follows every element of lower lanes and its own j' < j; ties at T
-// are kept in index order up to need when split. kMask: writes the 0/1
-// mask (every element of the row) instead of the index list and pair
-// counts. Returns the number kept.
+// are kept in index order up to need when split. The kept indices go to
+// stage[0 ..) in LDS (other lanes write their trash slot stage[64 EPT +
+// lane]) and, for VASC, into the pair counts (trash counters pair_cnt[P +
+// lane]). kMask: writes the 0/1 mask (every element of the row) instead.
+// Returns the number kept.
 template <bool kVasc, bool kMask, int EPT>
 __device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane, uint32_t T, int need, bool split,
-                                           bool none, uint32_t tsel, int64_t width, int32_t *irow,
-                                           uint32_t *pair_cnt, uint8_t *mrow) {
+                                           bool none, uint32_t tsel, uint32_t *stage, int P, uint32_t *pair_cnt,
+                                           uint8_t *mrow) {
   int run_sel = 0, run_eq = 0;
 #pragma unroll
   for (int i = 0; i < EPT / 4; ++i) {
@@ -494,11 +595,11 @@ __device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         eq[j] = key[4 * i + j] == T;
-        beq[j] = __ballot(eq[j]);
+        beq[j] = __builtin_amdgcn_ballot_w64(eq[j]);
       }
       int eq_rank = run_eq;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) eq_rank += __popcll(beq[j] & lanemask_lt());
+      for (int j = 0; j < 4; ++j) eq_rank += lanes_below(beq[j]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         sel[j] = key[4 * i + j] > T || (eq[j] && eq_rank < need);
@@ -520,16 +621,14 @@ __device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane,
       int pos = run_sel;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        bsel[j] = __ballot(sel[j]);
-        pos += __popcll(bsel[j] & lanemask_lt());
+        bsel[j] = __builtin_amdgcn_ballot_w64(sel[j]);
+        pos += lanes_below(bsel[j]);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (sel[j]) {
-          if (pos < width) irow[pos] = kk + j;
-          if (kVasc) atomicAdd(&pair_cnt[(kk + j) >> 1], 1u);
-          ++pos;
-        }
+        stage[sel[j] ? pos : 64 * EPT + lane] = static_cast<uint32_t>(kk + j);
+        if (kVasc) atomicAdd(&pair_cnt[sel[j] ? (kk + j) >> 1 : P + lane], 1u);
+        pos += sel[j] ? 1 : 0;
         run_sel += __popcll(bsel[j]);
       }
     }
@@ -538,8 +637,13 @@ __device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane,
 }
 
 // per wave: histogram (256 bins + 64 per-lane trash bins), small-bin keys
-// (64 + 64 per-lane trash slots)
-constexpr int kWaveLds = 256 + 64 + 128;
+// (64 + 64 per-lane trash slots), then 64 * (EPT + 1) words shared by the
+// bracket candidates (one segment of EPT + 1 per lane) and the staged index
+// list (K entries + 64 per-lane trash slots)
+template <int EPT>
+constexpr int wave_lds_words() {
+  return 256 + 64 + 128 + 64 * (EPT + 1);
+}
 
 // kWaves waves per workgroup, rows_per_wave consecutive rows per wave (all
 // rows of one head); LDS: the waves' histograms and small-bin buffers, then
@@ -549,14 +653,15 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int tid = threadIdx.x, lane0 = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  uint32_t *hist = lds + w * kWaveLds;
+  uint32_t *hist = lds + w * wave_lds_words<EPT>();
   uint32_t *sbuf = hist + 256 + 64;
-  uint32_t *pair_cnt = lds + kWaves * kWaveLds;
+  uint32_t *cand = sbuf + 128;
+  uint32_t *pair_cnt = lds + kWaves * wave_lds_words<EPT>();
   const int64_t bh = blockIdx.y;
   const int K = static_cast<int>(p.K);
   int gate = 0;
   if (kVasc) {
-    for (int64_t i = tid; i < p.P; i += 256) pair_cnt[i] = 0;
+    for (int64_t i = tid; i < p.P + 64; i += 256) pair_cnt[i] = 0;  // P pairs + 64 trash counters
     __syncthreads();
     gate = service_gate(p);
   }
@@ -615,6 +720,7 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
       last = order_key(srow[K - 1]);
     }
     uint32_t kmin = 0xffffffffu, kmax = 0u, kmaxh = 0u;
+    uint32_t rawmax = 0u;  // Top-K: largest raw score bits (sign set or NaN above 0x7f800000)
     int beat = 0;
     // Steps wholly before the last element need no per-element masks; only
     // the step holding the last element (K - 1) checks k < K and k == K - 1
@@ -649,9 +755,15 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
           if (p.protected_mask) kj = ok && p.protected_mask[row * p.K + k] ? top : kj;
           kj = p.force_last && is_last ? top : kj;
         } else {
-          kj = order_key(sv);
-          beat += ok && ((kj > last) || (kj == last && !is_last)) ? 1 : 0;
-          kj = p.force_last && is_last ? 0xffffffffu : kj;
+          // the raw bits with the sign flipped: the order key of any
+          // non-negative, non-NaN score (others are redone below)
+          const uint32_t raw = key[4 * i + j];
+          rawmax = ok && raw > rawmax ? raw : rawmax;
+          kj = raw ^ 0x80000000u;
+          if (p.force_last) {
+            beat += ok && ((kj > last) || (kj == last && !is_last)) ? 1 : 0;
+            kj = is_last ? 0xffffffffu : kj;
+          }
         }
         kj = ok ? kj : 0u;
         kmin = ok && kj < kmin ? kj : kmin;
@@ -666,6 +778,37 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
         transform(i, std::false_type{});
       else if (256 * i < K)
         transform(i, std::true_type{});
+    }
+    if (!kVasc) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t a = __shfl_xor(rawmax, o);
+        rawmax = a > rawmax ? a : rawmax;
+      }
+      if (__builtin_amdgcn_readfirstlane(rawmax) > 0x7f800000u) {
+        // a negative, -0 or NaN score: full order keys for the row
+        kmin = 0xffffffffu;
+        kmax = kmaxh = 0u;
+        beat = 0;
+#pragma unroll
+        for (int i = 0; i < EPT / 4; ++i) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int k = 256 * i + 4 * lane + j;
+            const bool ok = k < K;
+            uint32_t kj = order_key(__uint_as_float(key[4 * i + j] ^ 0x80000000u));
+            if (p.force_last) {
+              beat += ok && ((kj > last) || (kj == last && k != K - 1)) ? 1 : 0;
+              kj = k == K - 1 ? 0xffffffffu : kj;
+            }
+            kj = ok ? kj : 0u;
+            kmin = ok && kj < kmin ? kj : kmin;
+            kmax = kj > kmax ? kj : kmax;
+            kmaxh = kj != forced && kj > kmaxh ? kj : kmaxh;
+            key[4 * i + j] = kj;
+          }
+        }
+      }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -713,8 +856,33 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
       }
       if (bin_lo >= 0) lo = kmin + (static_cast<uint32_t>(bin_lo) << sh);
       if (lo > hm1) lo = kmin;
-      if (!rank_keys(key, lane, lo, hm1, c, hist, sbuf, T, need, eqT))
-        rank_keys(key, lane, kmin, kmax, c, hist, sbuf, T, need, eqT);  // missed bracket: the whole range
+      // candidates [lo, hm1] to LDS, each lane into its own segment (every
+      // key is written at the segment's end, which only advances past a
+      // candidate), keys above hm1 counted
+      uint32_t *seg = cand + lane * (EPT + 1);
+      int above = 0, cnt = 0;
+      const uint32_t span = hm1 - lo;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const uint32_t x = key[j];
+        above += x > hm1;
+        seg[cnt] = x;
+        cnt += x - lo <= span;  // key 0 (and anything below lo) wraps above span
+      }
+      above = __builtin_amdgcn_readfirstlane(wave_sum_int(above));
+      int n = cnt, maxcnt = cnt;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        n += __shfl_xor(n, o);
+        maxcnt = max(maxcnt, __shfl_xor(maxcnt, o));
+      }
+      n = __builtin_amdgcn_readfirstlane(n);
+      maxcnt = __builtin_amdgcn_readfirstlane(maxcnt);
+      wave_sync();
+      if (above < c && above + n >= c)
+        rank_segs(seg, cnt, maxcnt, lane, lo, hm1, c - above, hist, sbuf, T, need, eqT);
+      else  // missed bracket: rank the whole row
+        rank_keys(key, lane, kmin, kmax, c, hist, sbuf, T, need, eqT);
     }
     const bool split = !all && !none && need < eqT;
     const uint32_t tsel = all ? 1u : T;  // keys >= tsel are kept (no split)
@@ -723,10 +891,16 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
     // mask and priority outputs in passes of their own
     int32_t *irow = p.index_out + row * p.width;
     asm volatile("" : "+v"(lane));  // element indices recomputed here, not kept from the loads
-    const int run_sel = compact_row<kVasc, false, EPT>(key, lane, T, need, split, none, tsel, p.width, irow,
-                                                      pair_cnt, nullptr);
+    const int run_sel = compact_row<kVasc, false, EPT>(key, lane, T, need, split, none, tsel, cand,
+                                                      static_cast<int>(p.P), pair_cnt, nullptr);
+    wave_sync();
+    {
+      const int wn = run_sel < p.width ? run_sel : static_cast<int>(p.width);
+      for (int e = lane; e < wn; e += 64) irow[e] = static_cast<int32_t>(cand[e]);  // coalesced
+    }
+    wave_sync();  // the staged list is read before the next row reuses it
     if (p.mask_out)
-      compact_row<kVasc, true, EPT>(key, lane, T, need, split, none, tsel, p.width, nullptr, nullptr,
+      compact_row<kVasc, true, EPT>(key, lane, T, need, split, none, tsel, nullptr, 0, nullptr,
                                     p.mask_out + row * p.K);
     if (kVasc && p.priority_out) {
 #pragma unroll
@@ -806,7 +980,7 @@ int launch_select_cfg(const SelectParams &p, hipStream_t s) {
   // keep the global count atomics down.
   const int64_t rows = p.BH * p.Q;
   const int rpw = static_cast<int>(rows >= 4 * 8192 ? 4 : (rows >= 2 * 8192 ? 2 : 1));
-  const size_t lds = (static_cast<size_t>(kWaves) * kWaveLds + (kVasc ? static_cast<size_t>(p.P) : 0)) * 4;
+  const size_t lds = (static_cast<size_t>(kWaves) * wave_lds_words<EPT>() + (kVasc ? static_cast<size_t>(p.P) + 64 : 0)) * 4;
   const void *kern = reinterpret_cast<const void *>(select_kernel<kVasc, EPT>);
   int rc;
   if ((rc = reserve_lds(kern, lds))) return rc;
