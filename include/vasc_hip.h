@@ -193,6 +193,29 @@ int vasc_block_sparse_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
                                int32_t index_is_delta, float sm_scale,
                                void *stream);
 
+/*
+ * Kernel 4 for a whole global layer: the patch queries q_patch [B,H,n_patch,d]
+ * attend to their listed blocks as in vasc_block_sparse_attn_fwd (absolute
+ * indices), and the special-token queries q_special [B,H,n_special,d] attend
+ * to every key, in the same launch (attention.py:8464-8484 runs them through
+ * a separate dense SDPA). k [B,H,nk,d] and vt hold all tokens, patch tokens
+ * first. Outputs o_patch [B,H,n_patch,d], o_special [B,H,n_special,d]; all
+ * strided as in vasc_block_sparse_attn_fwd. n_special may be 0 (q_special,
+ * o_special then unused). Built variant: d == 64.
+ */
+int vasc_global_attn_fwd(const uint16_t *q_patch, int64_t qp_sb, int64_t qp_sh,
+                         int64_t qp_st, const uint16_t *q_special,
+                         int64_t qs_sb, int64_t qs_sh, int64_t qs_st,
+                         const uint16_t *k, int64_t k_sb, int64_t k_sh,
+                         int64_t k_st, const uint16_t *vt, uint16_t *o_patch,
+                         int64_t op_sb, int64_t op_sh, int64_t op_st,
+                         uint16_t *o_special, int64_t os_sb, int64_t os_sh,
+                         int64_t os_st, int64_t B, int64_t H, int64_t n_patch,
+                         int64_t n_special, int64_t nk, int64_t d,
+                         const int32_t *block_index, int64_t index_width,
+                         const int32_t *block_count, float sm_scale,
+                         void *stream);
+
 /* Dense variant of kernel 4: every query block attends to all key blocks. */
 int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
                         int64_t q_st, const uint16_t *k, int64_t k_sb,
@@ -200,6 +223,57 @@ int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
                         uint16_t *o, int64_t o_sb, int64_t o_sh, int64_t o_st,
                         int64_t B, int64_t H, int64_t nq, int64_t nk,
                         int64_t d, float sm_scale, void *stream);
+
+/*
+ * Kernel 5a: token layout of a global layer. Replaces the head split,
+ * q_norm / k_norm, rotary embedding and the [patch; special] reorder of
+ * attention.py:8351-8469 (tokens.py:2-62: six full copies) with one pass.
+ *
+ * q, k, v: frame-major tokens, T = N*P (per frame S special tokens, then
+ *   P-S patch tokens), element (b,t,h,j) at ptr + b*sb + t*st + h*sh + j
+ *   (j contiguous). The fused qkv projection [B,T,3*H*d] is q = qkv,
+ *   k = qkv + H*d, v = qkv + 2*H*d with st = 3*H*d, sh = d.
+ * q_norm / k_norm != 0: LayerNorm over the d features of each (token, head)
+ *   with optional weight and bias [d] (NULL: 1 / 0) and eps, before the
+ *   rotary embedding.
+ * pos != NULL: 2D rotary embedding of q and k. Token (b,t) has the integer
+ *   row / column position pos[b*pos_sb + t*pos_st + 0 / 1]; features
+ *   [0, d/2) rotate with the row, [d/2, d) with the column; inside a half,
+ *   feature j < d/4 pairs with j + d/4:
+ *     out_j      = x_j cos(a) - x_{j+d/4} sin(a)
+ *     out_{j+d/4} = x_{j+d/4} cos(a) + x_j sin(a),   a = position * freq_j
+ *   with cos/sin read from rope_cos / rope_sin [rope_n, d/4] (float32,
+ *   entry (position, j)); positions are clamped into [0, rope_n).
+ * Outputs (contiguous bf16): q_patch [B,H,N*(P-S),d], q_special [B,H,N*S,d],
+ *   k_out / v_out [B,H,T,d] with the patch tokens of all frames first, then
+ *   the special tokens. Arithmetic in float32, one bf16 rounding per output.
+ * Built variant: d == 64.
+ */
+int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                  const uint16_t *k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                  const uint16_t *v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                  int64_t B, int64_t H, int64_t N, int64_t P, int64_t S,
+                  int64_t d, const float *q_norm_w, const float *q_norm_b,
+                  float q_eps, int32_t q_norm, const float *k_norm_w,
+                  const float *k_norm_b, float k_eps, int32_t k_norm,
+                  const int32_t *pos, int64_t pos_sb, int64_t pos_st,
+                  const float *rope_cos, const float *rope_sin, int64_t rope_n,
+                  uint16_t *q_patch, uint16_t *q_special, uint16_t *k_out,
+                  uint16_t *v_out, void *stream);
+
+/*
+ * Kernel 5b: attention outputs in [patch; special] order back to the
+ * frame-major token layout the output projection reads (attention.py:
+ * 8992-9027 with tokens.py:102-126 and the transpose/reshape):
+ * out[b, t, h*d + j] from x_patch [B,H,N*(P-S),d] or x_special [B,H,N*S,d]
+ * (strided as (b, h, token)). out [B,N*P,H*d] contiguous bf16.
+ * Built variant: d == 64.
+ */
+int vasc_restore_tokens(const uint16_t *x_patch, int64_t p_sb, int64_t p_sh,
+                        int64_t p_st, const uint16_t *x_special, int64_t s_sb,
+                        int64_t s_sh, int64_t s_st, int64_t B, int64_t H,
+                        int64_t N, int64_t P, int64_t S, int64_t d,
+                        uint16_t *out, void *stream);
 
 #ifdef __cplusplus
 }

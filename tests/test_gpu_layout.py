@@ -1,0 +1,195 @@
+"""Kernel 5 (token layout) and the whole-layer attention launch vs the oracle.
+
+Layout without norm/rotation moves bf16 values and is bit-exact. With the
+per-head LayerNorm and the 2D rotary embedding the kernel computes in
+float32 and rounds once to bf16: within one bf16 rounding of the float64
+oracle plus the float32 error (|err| <= 2^-8 |ref| + 1e-5).
+Attention tolerances as elsewhere: max-abs 2e-2, mean-abs 2e-3 vs float64.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import layout as OL
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy()
+
+
+def _bf16(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _to_np(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("N,P,S,H", [(3, 1041, 5, 2), (2, 37, 0, 3), (4, 6, 6, 1), (1, 131, 4, 16)])
+def test_pack_layout_bit_exact(N, P, S, H):
+    from vasc_amd import ops
+    D = 64
+    qkv = _bf16((1, N * P, 3 * H * D), N * 100 + P)
+    x = qkv.cuda().view(1, N * P, 3, H, D)
+    qp, qs, k, v = ops.pack_qkv(x[:, :, 0], x[:, :, 1], x[:, :, 2], N, P, S)
+    rp, rs, rk, rv = OL.pack_layer(qkv.float().numpy(), N, P, S, H)
+    assert np.array_equal(_to_np(qp), rp)
+    assert np.array_equal(_to_np(k), rk) and np.array_equal(_to_np(v), rv)
+    if S:
+        assert np.array_equal(_to_np(qs), rs)
+    else:
+        assert qs is None
+
+
+def test_pack_from_head_major_views():
+    """q/k/v given as [B,H,T,D] tensors (transposed views) instead of one qkv buffer."""
+    from vasc_amd import ops
+    N, P, S, H, D = 2, 300, 5, 4, 64
+    q, k, v = (_bf16((2, H, N * P, D), s) for s in (1, 2, 3))
+    qp, qs, ko, vo = ops.pack_qkv(*(t.cuda().transpose(1, 2) for t in (q, k, v)), N, P, S)
+    assert np.array_equal(_to_np(qp), OL.get_patch_tokens(q.float().numpy(), N, P, S))
+    assert np.array_equal(_to_np(qs), OL.get_special_tokens(q.float().numpy(), N, P, S))
+    assert np.array_equal(_to_np(ko), OL.reorder_to_patch_then_special(k.float().numpy(), N, P, S))
+    assert np.array_equal(_to_np(vo), OL.reorder_to_patch_then_special(v.float().numpy(), N, P, S))
+
+
+def test_pack_norm_and_rotary():
+    from vasc_amd import ops
+    from vasc_amd.aggregator import RotaryPositionEmbedding2D
+    N, Hp, Wp, S, H, D = 3, 9, 13, 5, 2, 64
+    P = Hp * Wp + S
+    qkv = _bf16((1, N * P, 3 * H * D), 7, 2.0)
+    g = torch.Generator().manual_seed(8)
+    qw, qb, kw = (torch.randn(D, generator=g) for _ in range(3))
+    ys, xs = torch.meshgrid(torch.arange(Hp), torch.arange(Wp), indexing="ij")
+    frame_pos = torch.cat([torch.zeros(S, 2, dtype=torch.long), torch.stack([ys.reshape(-1), xs.reshape(-1)], -1) + 1])
+    pos = frame_pos.repeat(N, 1)  # [T, 2]
+    cos, sin = RotaryPositionEmbedding2D().tables(int(pos.max()) + 1, D, "cuda")
+    x = qkv.cuda().view(1, N * P, 3, H, D)
+    qp, qs, k, v = ops.pack_qkv(x[:, :, 0], x[:, :, 1], x[:, :, 2], N, P, S, q_norm=(qw.cuda(), qb.cuda(), 1e-6),
+                                k_norm=(kw.cuda(), None, 1e-5), pos=pos.cuda(), rope_tables=(cos, sin))
+    rp, rs, rk, rv = OL.pack_layer(qkv.float().numpy(), N, P, S, H, q_norm=(qw.numpy(), qb.numpy(), 1e-6),
+                                   k_norm=(kw.numpy(), None, 1e-5), pos=pos.numpy(),
+                                   tables=(cos.cpu().numpy(), sin.cpu().numpy()))
+    for got, ref in ((qp, rp), (qs, rs), (k, rk)):
+        err = np.abs(_to_np(got) - ref)
+        assert (err <= np.abs(ref) * 2.0 ** -8 + 1e-5).all(), err.max()
+    assert np.array_equal(_to_np(v), rv)
+
+
+@pytest.mark.parametrize("N,P,S", [(3, 1041, 5), (2, 50, 0), (2, 7, 7)])
+def test_restore_bit_exact(N, P, S):
+    from vasc_amd import ops
+    H, D = 3, 64
+    xp = _bf16((2, H, N * (P - S), D), 11)
+    xs = _bf16((2, H, N * S, D), 12) if S else None
+    out = ops.restore_tokens(xp.cuda(), xs.cuda() if S else None, N, P, S)
+    re = xp.float().numpy() if not S else np.concatenate([xp.float().numpy(), xs.float().numpy()], axis=2)
+    ref = OL.restore_to_frame_major(re, N, P, S).transpose(0, 2, 1, 3).reshape(2, N * P, H * D)
+    assert np.array_equal(_to_np(out), ref)
+
+
+def test_global_attn_patch_and_special_in_one_launch():
+    """Patch rows: bit-identical to the block-sparse entry point on the same
+    lists; special rows: bit-identical to the dense entry point and within
+    tolerance of the float64 oracle."""
+    from vasc_amd import ops
+    B, H, Np, Ns, D = 1, 3, 2000, 150, 64
+    Tk = Np + Ns
+    q = _bf16((B, H, Np, D), 21).cuda()
+    qs = _bf16((B, H, Ns, D), 22).cuda()
+    k = _bf16((B, H, Tk, D), 23).cuda()
+    v = _bf16((B, H, Tk, D), 24).cuda()
+    nkb, qb = math.ceil(Tk / 64), math.ceil(Np / 128)
+    rng = np.random.default_rng(25)
+    idx = np.full((B, H, qb, nkb), -1, np.int32)
+    cnt = rng.integers(1, nkb + 1, size=(B, H, qb)).astype(np.int32)
+    for h in range(H):
+        for i in range(qb):
+            idx[0, h, i, : cnt[0, h, i]] = np.sort(rng.choice(nkb, cnt[0, h, i], replace=False))
+    index, count = torch.from_numpy(idx).cuda(), torch.from_numpy(cnt).cuda()
+    vt = ops.pack_v(v)
+    o_p, o_s = ops.global_attn(q, qs, k, vt, index, count)
+    assert np.array_equal(_bits(o_p), _bits(ops.block_sparse_attn(q, k, vt, index, count)))
+    assert np.array_equal(_bits(o_s), _bits(ops.dense_attn(qs, k, vt)))
+    dl, dc = OA.dense_lists(B, H, Ns, Tk)
+    ref = OA.block_sparse_attention(qs.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                                    dl, dc)
+    err = np.abs(_to_np(o_s) - ref)
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
+    o_p2, none = ops.global_attn(q, None, k, vt, index, count)
+    assert none is None and np.array_equal(_bits(o_p2), _bits(o_p))
+
+
+def test_global_layer_sparse_matches_oracle_layer():
+    """The fused layer forward (layout kernel with LayerNorm + rotary, pooled
+    predictor, Top-K selection, one attention launch, restore) against the
+    oracle's layer on the same module: the index lists come from the GPU
+    selection and the oracle recomputes attention over exactly those blocks."""
+    import os
+    from vasc_amd import ops
+    from vasc_amd.aggregator import Attention, RotaryPositionEmbedding2D
+    from vasc_amd.attention import adaptive_sparse_attention_forward, predict_attention
+    from vasc_amd.sparse_wrapper import get_block_mask
+
+    torch.manual_seed(31)
+    N, Hp, Wp, S, heads, dim = 4, 11, 13, 5, 4, 256
+    P = Hp * Wp + S
+    m = Attention(dim, heads, rope=RotaryPositionEmbedding2D()).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        m.q_norm.weight.normal_(1.0, 0.2)
+        m.k_norm.bias.normal_(0.0, 0.2)
+    x = torch.randn(1, N * P, dim, device="cuda", dtype=torch.bfloat16)
+    ys, xs = torch.meshgrid(torch.arange(Hp), torch.arange(Wp), indexing="ij")
+    frame_pos = torch.cat([torch.zeros(S, 2, dtype=torch.long), torch.stack([ys.reshape(-1), xs.reshape(-1)], -1) + 1])
+    pos = frame_pos.repeat(N, 1).unsqueeze(0).cuda()
+    saved = {kk: os.environ.pop(kk) for kk in list(os.environ) if kk.startswith("SPARSE_VGGT_")}
+    try:
+        os.environ["SPARSE_VGGT_OFFICIAL_MASK"] = "1"
+        with torch.no_grad():
+            out = adaptive_sparse_attention_forward(m, x, pos, sparse_ratio=0.5, num_special_tokens=S,
+                                                    num_heads=heads, routing_state={})
+            qkv = m.qkv(x)
+            cos, sin = m.rope.tables(int(pos.max()) + 1, dim // heads, "cuda")
+            qp, qsp, kre, vre = OL.pack_layer(
+                qkv.float().cpu().numpy(), N, P, S, heads,
+                q_norm=(m.q_norm.weight.float().cpu().numpy(), m.q_norm.bias.float().cpu().numpy(), m.q_norm.eps),
+                k_norm=(m.k_norm.weight.float().cpu().numpy(), m.k_norm.bias.float().cpu().numpy(), m.k_norm.eps),
+                pos=pos[0].cpu().numpy(), tables=(cos.cpu().numpy(), sin.cpu().numpy()))
+            # the selection the layer made, from the GPU pooled scores of the same packed q/k
+            gq, _, gk, _ = ops.pack_qkv(*(qkv.view(1, N * P, 3, heads, dim // heads)[:, :, i] for i in range(3)),
+                                        N, P, S, q_norm=(m.q_norm.weight, m.q_norm.bias, m.q_norm.eps),
+                                        k_norm=(m.k_norm.weight, m.k_norm.bias, m.k_norm.eps), pos=pos,
+                                        rope_tables=(cos, sin))
+            n_patch = N * (P - S)
+            score = predict_attention(gq, gk[:, :, :n_patch])
+            sink = math.ceil(N * P / 64) - score.shape[-1]
+            mask = get_block_mask(score, sink, sparse_ratio=0.5)
+    finally:
+        os.environ.pop("SPARSE_VGGT_OFFICIAL_MASK", None)
+        os.environ.update(saved)
+    mk = mask.cpu().numpy()
+    Qb = mk.shape[2]
+    W = mk.shape[3]
+    idx = np.full((1, heads, Qb, W), -1, np.int32)
+    cnt = mk.sum(-1).astype(np.int32)
+    for h in range(heads):
+        for i in range(Qb):
+            sel = np.nonzero(mk[0, h, i])[0]
+            idx[0, h, i, : sel.size] = sel
+    bf = lambda a: torch.from_numpy(a).to(torch.bfloat16).float().numpy()  # noqa: E731  (inputs as the GPU sees them)
+    o_p = OA.block_sparse_attention(bf(qp), bf(kre), bf(vre), idx, cnt)
+    dl, dc = OA.dense_lists(1, heads, N * S, N * P)
+    o_s = OA.block_sparse_attention(bf(qsp), bf(kre), bf(vre), dl, dc)
+    o = OL.restore_to_frame_major(np.concatenate([o_p, o_s], axis=2), N, P, S)
+    o = torch.from_numpy(o.transpose(0, 2, 1, 3).reshape(1, N * P, dim)).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        ref = m.proj(o).float()
+    err = (out.float() - ref).abs()
+    assert err.max() < 6e-2 and err.mean() < 6e-3, (err.max().item(), err.mean().item())

@@ -71,7 +71,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES), "ctypes table out of sync with include/vasc_hip.h"
-    assert lib.vasc_abi_version() == 1
+    assert lib.vasc_abi_version() == 2
 
 
 def test_host_only_queries_and_argument_errors():
@@ -98,3 +98,20 @@ def test_host_only_queries_and_argument_errors():
     assert rc == 1
     with pytest.raises(_lib.VascArgumentError):
         _lib.call("vasc_settle_terminal", None, None, None, 0, None, None)
+    # token layout: sizes and pointers are checked before any launch
+    f = ctypes.c_float
+    rc = lib.vasc_pack_qkv(None, 0, 3072, 64, None, 0, 3072, 64, None, 0, 3072, 64, 1, 16, 2, 1041, 5, 64,
+                           None, None, f(1e-6), 0, None, None, f(1e-6), 0, None, 0, 2, None, None, 0,
+                           None, None, None, None, None)
+    assert rc == 1 and b"q is NULL" in lib.vasc_last_error()
+    rc = lib.vasc_pack_qkv(None, 0, 3072, 64, None, 0, 3072, 64, None, 0, 3072, 64, 1, 16, 2, 1041, 5, 128,
+                           None, None, f(1e-6), 0, None, None, f(1e-6), 0, None, 0, 2, None, None, 0,
+                           None, None, None, None, None)
+    assert rc == 2 and b"head_dim" in lib.vasc_last_error()
+    rc = lib.vasc_restore_tokens(None, 0, 0, 8, None, 0, 0, 8, 1, 16, 2, 1041, 5, 64, None, None)
+    assert rc == 1 and b"out must be" in lib.vasc_last_error()
+    rc = lib.vasc_restore_tokens(None, 0, 0, 8, None, 0, 0, 8, 1, 16, 2, 4, 5, 64, None, None)
+    assert rc == 1 and b"invalid sizes" in lib.vasc_last_error()
+    rc = lib.vasc_global_attn_fwd(None, 0, 0, 8, None, 0, 0, 8, None, 0, 0, 8, None, None, 0, 0, 8,
+                                  None, 0, 0, 8, 1, 1, 128, 32, 64, 64, None, 1, None, f(0.125), None)
+    assert rc == 1 and b"q_special" in lib.vasc_last_error()

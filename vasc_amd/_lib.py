@@ -40,6 +40,14 @@ SIGNATURES: dict[str, tuple] = {
                                              I64, I64, I64, I64, I64, P, I64, P, I32, c_float, P]),
     "vasc_dense_attn_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, P, I64, I64, I64,
                                       I64, I64, I64, I64, I64, c_float, P]),
+    "vasc_global_attn_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64, P,
+                                       P, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64, I64, I64,
+                                       P, I64, P, c_float, P]),
+    "vasc_pack_qkv": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64,
+                                I64, I64, I64, I64, I64, I64, P, P, c_float, I32, P, P, c_float, I32,
+                                P, I64, I64, P, P, I64, P, P, P, P, P]),
+    "vasc_restore_tokens": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64, I64, I64,
+                                      P, P]),
 }
 
 _lock = threading.Lock()

@@ -16,8 +16,6 @@ import math
 import torch
 
 from . import ops
-from .sparse_wrapper import block_sparse_attn_cuda
-from .tokens import get_patch_tokens, get_special_tokens, reorder_to_patch_then_special, restore_to_frame_major
 
 
 def predict_attention(query: torch.Tensor, key: torch.Tensor, ks_q: int = 128, ks_k: int = 64,
@@ -59,39 +57,45 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
 
     ``self`` provides ``qkv``, ``q_norm``, ``k_norm``, optional ``rope`` and
     ``proj`` / ``proj_drop`` (the upstream VGGT/Pi3 attention module).
+
+    The head split, q/k norms, rotary embedding and [patch; special] reorder
+    (ATT:8351-8469) are one layout kernel when the norms are per-head
+    LayerNorms (or identities) and the rope is ``RotaryPositionEmbedding2D``;
+    other modules run their norms and rope in torch first. Special-token
+    queries attend to every key in the same launch as the patch queries, and
+    one kernel restores the frame-major order before ``proj`` (ATT:8992-9030).
     """
+    from .aggregator import fused_layout_supported, layer_norm_args
+    from .sparse_wrapper import sparse_global_attention
+
     if routing_state is None:
         routing_state = getattr(self, "_sparse_routing_state", None)
     B, NP, dim = x.shape
     S, nh = num_special_tokens, num_heads
     hd = dim // nh
     Hp, Wp, N, P = _infer_frames(pos, NP, S)
-    qkv = self.qkv(x).reshape(B, NP, 3, nh, hd).permute(2, 0, 3, 1, 4)
-    q, k, v = qkv.unbind(0)
-    q, k = self.q_norm(q), self.k_norm(k)
-    if getattr(self, "rope", None) is not None:
-        q = self.rope(q, pos)
-        k = self.rope(k, pos)
-    k_re = reorder_to_patch_then_special(k, N, P, S)
-    v_re = reorder_to_patch_then_special(v, N, P, S)
-    q_patch = get_patch_tokens(q, N, P, S)
-    q_special = get_special_tokens(q, N, P, S)
+    qkv = self.qkv(x).to(torch.bfloat16).view(B, NP, 3, nh, hd)
+    rope = getattr(self, "rope", None)
+    if fused_layout_supported(self):
+        tables = rope.tables(int(pos.max()) + 1, hd, x.device) if rope is not None else None
+        q_patch, q_special, k_re, v_re = ops.pack_qkv(
+            qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], N, P, S, q_norm=layer_norm_args(self.q_norm),
+            k_norm=layer_norm_args(self.k_norm), pos=pos if rope is not None else None, rope_tables=tables)
+    else:
+        q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+        q, k = self.q_norm(q), self.k_norm(k)
+        if rope is not None:
+            q, k = rope(q, pos), rope(k, pos)
+        q_patch, q_special, k_re, v_re = ops.pack_qkv(
+            *(t.to(torch.bfloat16).transpose(1, 2) for t in (q, k, v)), N, P, S)
     n_patch = N * (P - S)
-    scale = 1.0 / math.sqrt(hd)
-    x_special = None
-    if q_special is not None:
-        # every special query attends to all tokens: the dense MFMA kernel
-        x_special = ops.dense_attn(q_special, k_re, ops.pack_v(v_re), scale=scale).to(q.dtype)
     attn_pooled = predict_attention(q_patch, k_re[:, :, :n_patch], pool_mode=pool_mode)
-    x_patch, sparsity = block_sparse_attn_cuda(q_patch, k_re, v_re, attn_pooled, sparse_ratio=sparse_ratio,
-                                               cdf_threshold=cdf_threshold, return_sparsity=True,
-                                               layer_idx=layer_idx, routing_state=routing_state,
-                                               num_patch_tokens=n_patch, **research)
+    x_patch, x_special, sparsity = sparse_global_attention(
+        q_patch, q_special, k_re, v_re, attn_pooled, sparse_ratio=sparse_ratio, cdf_threshold=cdf_threshold,
+        layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch, **research)
     if aux_output_store is not None:
         aux_output_store["sparsity"] = sparsity
-    x_re = torch.cat([x_patch.to(q.dtype), x_special], dim=-2) if x_special is not None else x_patch.to(q.dtype)
-    out = restore_to_frame_major(x_re, N, P, S)
-    out = out.transpose(1, 2).reshape(B, NP, nh * hd)
-    out = self.proj(out)
+    out = ops.restore_tokens(x_patch, x_special, N, P, S)
+    out = self.proj(out.to(x.dtype))
     drop = getattr(self, "proj_drop", None)
     return drop(out) if drop is not None else out

@@ -33,6 +33,11 @@
 //    buffer being read and would drain it before every LDS read.
 //  * workgroup ids are remapped so each XCD walks a contiguous range of
 //    query blocks of the same head (K/V reuse in that XCD's L2).
+//  * vasc_global_attn_fwd adds the layer's special-token queries, which
+//    attend to every key (attention.py:8480-8484), to the same launch: their
+//    workgroups take the first hardware ids, so they spread over all XCDs
+//    and start first (each walks every key block, about four times the
+//    work of a patch-query workgroup).
 #include "common.h"
 
 namespace vasc {
@@ -59,6 +64,12 @@ struct AttnParams {
   int32_t delta;
   float c;  // sm_scale * log2(e)
   int64_t num_wg;
+  // special-token queries (dense over every key block), NULL when absent
+  const uint16_t *q2;
+  int64_t q2_sb, q2_sh, q2_st;
+  uint16_t *o2;
+  int64_t o2_sb, o2_sh, o2_st;
+  int64_t nq2, nq2b, num_wg2;
 };
 
 __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
@@ -88,9 +99,14 @@ void bsattn_fwd_kernel(const AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][kTile];  // [buffer][K, Vt]
   auto lds_u32 = [](const uint16_t *ptr) { return lds_addr32(ptr); };
 
-  const int64_t wg = xcd_remap(blockIdx.x, p.num_wg);
-  const int qb = static_cast<int>(wg % p.nqb);
-  const int64_t bh = wg / p.nqb;
+  // Workgroups [0, num_wg2) take the special-token queries (every key
+  // block); the rest the patch queries of their lists.
+  const bool dense = kDense || static_cast<int64_t>(blockIdx.x) < p.num_wg2;
+  const int64_t nqb = dense && !kDense ? p.nq2b : p.nqb;
+  const int64_t wg = dense && !kDense ? static_cast<int64_t>(blockIdx.x)
+                                      : xcd_remap(static_cast<int64_t>(blockIdx.x) - p.num_wg2, p.num_wg);
+  const int qb = static_cast<int>(wg % nqb);
+  const int64_t bh = wg / nqb;
   const int64_t h = bh % p.H;
   const int64_t b = bh / p.H;
   const int tid = threadIdx.x;
@@ -99,7 +115,7 @@ void bsattn_fwd_kernel(const AttnParams p) {
 
   int n;
   const int32_t *list = nullptr;
-  if (kDense) {
+  if (dense) {
     n = static_cast<int>(p.nkb);
   } else {
     const int64_t row = bh * p.nqb + qb;
@@ -108,9 +124,15 @@ void bsattn_fwd_kernel(const AttnParams p) {
     n = n < 0 ? 0 : (n > p.idx_w ? static_cast<int>(p.idx_w) : n);
   }
 
+  const bool sp = dense && !kDense;  // a special-query workgroup
+  const uint16_t *qsrc = sp ? p.q2 : p.q;
+  const int64_t q_sb = sp ? p.q2_sb : p.q_sb, q_sh = sp ? p.q2_sh : p.q_sh, q_st = sp ? p.q2_st : p.q_st;
+  const int64_t nq = sp ? p.nq2 : p.nq;
+  uint16_t *odst = sp ? p.o2 : p.o;
+  const int64_t o_sb = sp ? p.o2_sb : p.o_sb, o_sh = sp ? p.o2_sh : p.o_sh, o_st = sp ? p.o2_st : p.o_st;
   const int64_t qrow = static_cast<int64_t>(qb) * kBlockQ + w * 32 + lr;
-  const bool qvalid = qrow < p.nq;
-  uint16_t *optr = p.o + b * p.o_sb + h * p.o_sh + (qvalid ? qrow : 0) * p.o_st;
+  const bool qvalid = qrow < nq;
+  uint16_t *optr = odst + b * o_sb + h * o_sh + (qvalid ? qrow : 0) * o_st;
 
   if (n == 0) {
     if (qvalid) {
@@ -123,7 +145,7 @@ void bsattn_fwd_kernel(const AttnParams p) {
   // Q as the B operand of S^T = K Q^T: lane holds row lr, d = 16s + 8hf .. +7.
   u32x4 qf[4];
   {
-    const uint16_t *qptr = p.q + b * p.q_sb + h * p.q_sh + (qvalid ? qrow : 0) * p.q_st;
+    const uint16_t *qptr = qsrc + b * q_sb + h * q_sh + (qvalid ? qrow : 0) * q_st;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       qf[s] = qvalid ? *reinterpret_cast<const u32x4 *>(qptr + 16 * s + 8 * hf) : u32x4{0, 0, 0, 0};
@@ -240,8 +262,8 @@ void bsattn_fwd_kernel(const AttnParams p) {
   // List entry j+1 is loaded during iteration j-1 (index clamped to the list)
   // so that reading it never waits on memory: the wait at the top of each
   // iteration already covers it.
-  int blk = kDense ? 0 : __builtin_amdgcn_readfirstlane(list[0]);
-  int32_t e_next = kDense ? 0 : list[n > 1 ? 1 : 0];
+  int blk = dense ? 0 : __builtin_amdgcn_readfirstlane(list[0]);
+  int32_t e_next = dense ? 0 : list[n > 1 ? 1 : 0];
   fetch(blk, 0);
   for (int j = 0; j < n; ++j) {
     const int buf = j & 1;
@@ -249,7 +271,7 @@ void bsattn_fwd_kernel(const AttnParams p) {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     const int cur = blk;
     if (j + 1 < n) {
-      if (kDense) {
+      if (dense) {
         blk = j + 1;
       } else {
         const int e = __builtin_amdgcn_readfirstlane(e_next);
@@ -313,11 +335,21 @@ int check_bhtd(const char *name, const void *ptr, int64_t sb, int64_t sh, int64_
   return VASC_OK;
 }
 
+// Special-token queries of vasc_global_attn_fwd (absent: q2 == NULL).
+struct SpecialQueries {
+  const uint16_t *q2 = nullptr;
+  int64_t q2_sb = 0, q2_sh = 0, q2_st = 0;
+  uint16_t *o2 = nullptr;
+  int64_t o2_sb = 0, o2_sh = 0, o2_st = 0;
+  int64_t nq2 = 0;
+};
+
 int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                 const uint16_t *k, int64_t k_sb, int64_t k_sh, int64_t k_st, const uint16_t *vt,
                 uint16_t *o, int64_t o_sb, int64_t o_sh, int64_t o_st, int64_t B, int64_t H,
                 int64_t nq, int64_t nk, int64_t d, const int32_t *idx, int64_t idx_w,
-                const int32_t *cnt, int32_t delta, float sm_scale, void *stream) {
+                const int32_t *cnt, int32_t delta, float sm_scale, void *stream,
+                const SpecialQueries &sq = SpecialQueries()) {
   VASC_SUPPORTED(d == kHeadDim, "head_dim %lld not built (built: 64)", (long long)d);
   VASC_REQUIRE(B > 0 && H > 0 && nq > 0 && nk > 0, "sizes must be positive");
   int rc;
@@ -341,12 +373,17 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
   p.idx = idx; p.idx_w = idx_w; p.cnt = cnt; p.delta = delta;
   p.c = sm_scale * 1.4426950408889634f;
   p.num_wg = B * H * p.nqb;
-  VASC_REQUIRE(p.num_wg < (int64_t(1) << 31), "grid too large");
+  p.q2 = sq.q2; p.q2_sb = sq.q2_sb; p.q2_sh = sq.q2_sh; p.q2_st = sq.q2_st;
+  p.o2 = sq.o2; p.o2_sb = sq.o2_sb; p.o2_sh = sq.o2_sh; p.o2_st = sq.o2_st;
+  p.nq2 = sq.q2 ? sq.nq2 : 0;
+  p.nq2b = cdiv(p.nq2, kBlockQ);
+  p.num_wg2 = B * H * p.nq2b;
+  VASC_REQUIRE(p.num_wg + p.num_wg2 < (int64_t(1) << 31), "grid too large");
   VASC_SUPPORTED(nk < (int64_t(1) << 30) && nq < (int64_t(1) << 40), "sequence of %lld keys not built (< 2^30)",
                  (long long)nk);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   auto kern = dense ? bsattn_fwd_kernel<true> : bsattn_fwd_kernel<false>;
-  hipLaunchKernelGGL(kern, dim3(p.num_wg), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL(kern, dim3(p.num_wg + p.num_wg2), dim3(kThreads), 0, s, p);
   return check_launch(dense ? "vasc_dense_attn_fwd" : "vasc_block_sparse_attn_fwd");
 }
 
@@ -372,4 +409,27 @@ extern "C" int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh
                                    void *stream) {
   return vasc::launch_attn(true, q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, vt, o, o_sb, o_sh, o_st, B, H, nq,
                            nk, d, nullptr, 1, nullptr, 0, sm_scale, stream);
+}
+
+extern "C" int vasc_global_attn_fwd(const uint16_t *q_patch, int64_t qp_sb, int64_t qp_sh, int64_t qp_st,
+                                    const uint16_t *q_special, int64_t qs_sb, int64_t qs_sh, int64_t qs_st,
+                                    const uint16_t *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                    const uint16_t *vt, uint16_t *o_patch, int64_t op_sb, int64_t op_sh,
+                                    int64_t op_st, uint16_t *o_special, int64_t os_sb, int64_t os_sh,
+                                    int64_t os_st, int64_t B, int64_t H, int64_t n_patch, int64_t n_special,
+                                    int64_t nk, int64_t d, const int32_t *block_index, int64_t index_width,
+                                    const int32_t *block_count, float sm_scale, void *stream) {
+  using namespace vasc;
+  SpecialQueries sq;
+  if (n_special > 0) {
+    int rc;
+    if ((rc = check_bhtd("q_special", q_special, qs_sb, qs_sh, qs_st))) return rc;
+    if ((rc = check_bhtd("o_special", o_special, os_sb, os_sh, os_st))) return rc;
+    sq.q2 = q_special; sq.q2_sb = qs_sb; sq.q2_sh = qs_sh; sq.q2_st = qs_st;
+    sq.o2 = o_special; sq.o2_sb = os_sb; sq.o2_sh = os_sh; sq.o2_st = os_st;
+    sq.nq2 = n_special;
+  }
+  VASC_REQUIRE(n_special >= 0, "n_special must be non-negative");
+  return launch_attn(false, q_patch, qp_sb, qp_sh, qp_st, k, k_sb, k_sh, k_st, vt, o_patch, op_sb, op_sh, op_st,
+                     B, H, n_patch, nk, d, block_index, index_width, block_count, 0, sm_scale, stream, sq);
 }

@@ -1,0 +1,230 @@
+// Kernel 5: token layout of the global-attention layer.
+//
+// The reference layer (attention.py:8351-8484, 8992-9030; tokens.py:2-126)
+// splits the qkv projection into heads, applies q_norm / k_norm and the 2D
+// rotary embedding, then makes six full copies to reach the [all patch
+// tokens; all special tokens] order (reorder of q, k, v and extraction of
+// the patch queries) and two more to return to frame-major order before the
+// output projection. Here one pass reads each input element once and writes
+// it once in its final place:
+//
+//   pack     q, k, v (frame-major: per frame S special tokens, then P-S
+//            patch tokens) -> q_patch [B,H,Np,64], q_special [B,H,Ns,64],
+//            k and v [B,H,T,64] in [patch; special] order, with optional
+//            per-head LayerNorm of q and k and optional 2D rotary embedding,
+//            in that order (fp32 arithmetic, one bf16 rounding per output);
+//   restore  attention outputs in [patch; special] order -> frame-major
+//            [B,T,H*64] (the layer's transpose + reshape before proj).
+//
+// Eight lanes own one (token, tensor, head) row of 64 features, 8 per lane,
+// so a row is one 128-byte segment on both sides; the LayerNorm sums are
+// xor butterflies inside the 8-lane group and the rotary partner of a
+// feature (16 places away inside its half) sits two lanes away.
+// Precedent in the reference: kernels/qkv_layout.py:8-157 (layout only).
+#include "common.h"
+
+namespace vasc {
+namespace {
+
+constexpr int kHeadDim = 64;
+constexpr int kThreads = 256;
+constexpr int kRowsPerWg = kThreads / 8;
+
+struct PackParams {
+  const uint16_t *src[3];       // q, k, v: element (b, t, h, d) at src + b*sb + t*st + h*sh + d
+  int64_t sb[3], st[3], sh[3];
+  int64_t B, H, N, P, S;        // T = N * P frame-major tokens
+  const float *norm_w[2], *norm_b[2];
+  float eps[2];
+  int32_t norm[2];              // LayerNorm of q (0) and k (1)
+  const int32_t *pos;           // (row, column) position of token (b, t) at pos + b*pos_sb + t*pos_st
+  int64_t pos_sb, pos_st;
+  const float *rope_cos, *rope_sin;  // [rope_n, 16]: cos/sin of position p times frequency i
+  int64_t rope_n;
+  uint16_t *q_patch, *q_special, *k_out, *v_out;
+  int64_t rows;                 // B * T * 3 * H
+};
+
+__device__ __forceinline__ float group8_sum(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  return v;
+}
+
+__global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerWg + (threadIdx.x >> 3);
+  if (row >= p.rows) return;  // whole 8-lane groups leave together
+  const int sub = threadIdx.x & 7;
+  const int64_t h = row % p.H;
+  const int part = static_cast<int>((row / p.H) % 3);
+  const int64_t bt = row / (3 * p.H);
+  const int64_t T = p.N * p.P;
+  const int64_t t = bt % T, b = bt / T;
+
+  const u32x4 raw = *reinterpret_cast<const u32x4 *>(p.src[part] + b * p.sb[part] + t * p.st[part] +
+                                                    h * p.sh[part] + sub * 8);
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = bf16_to_f32(static_cast<uint16_t>(raw[e]));
+    x[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(raw[e] >> 16));
+  }
+  if (part < 2 && p.norm[part]) {
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += x[e];
+    const float mean = group8_sum(s) / static_cast<float>(kHeadDim);
+    float v = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v += (x[e] - mean) * (x[e] - mean);
+    const float var = group8_sum(v) / static_cast<float>(kHeadDim);
+    const float rstd = 1.0f / sqrtf(var + p.eps[part]);
+    const float *w = p.norm_w[part], *bb = p.norm_b[part];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float y = (x[e] - mean) * rstd;
+      if (w) y = y * w[sub * 8 + e];
+      if (bb) y = y + bb[sub * 8 + e];
+      x[e] = y;
+    }
+  }
+  if (part < 2 && p.pos) {
+    // features [0, 32) rotate with the row position, [32, 64) with the
+    // column position; inside a half, feature j < 16 pairs with j + 16
+    const int32_t *pp = p.pos + b * p.pos_sb + t * p.pos_st;
+    int64_t pq = pp[sub >> 2];
+    pq = pq < 0 ? 0 : (pq >= p.rope_n ? p.rope_n - 1 : pq);
+    const bool first = (sub & 2) == 0;
+    float partner[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) partner[e] = __shfl_xor(x[e], 2);
+    const float *cs = p.rope_cos + pq * 16 + (sub & 1) * 8;
+    const float *sn = p.rope_sin + pq * 16 + (sub & 1) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float rot = first ? -partner[e] : partner[e];
+      x[e] = x[e] * cs[e] + rot * sn[e];
+    }
+  }
+  u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(x[2 * e], x[2 * e + 1]);
+
+  const int64_t n = t / p.P, tf = t % p.P;
+  const int64_t np = p.N * (p.P - p.S), ns = p.N * p.S;
+  const bool patch = tf >= p.S;
+  const int64_t ip = n * (p.P - p.S) + (tf - p.S), is = n * p.S + tf;
+  uint16_t *dst;
+  if (part == 0)
+    dst = patch ? p.q_patch + ((b * p.H + h) * np + ip) * kHeadDim : p.q_special + ((b * p.H + h) * ns + is) * kHeadDim;
+  else
+    dst = (part == 1 ? p.k_out : p.v_out) + ((b * p.H + h) * T + (patch ? ip : np + is)) * kHeadDim;
+  *reinterpret_cast<u32x4 *>(dst + sub * 8) = out;
+}
+
+struct RestoreParams {
+  const uint16_t *xp, *xs;      // [B,H,Np,64] and [B,H,Ns,64], element (b,h,i,d) at x + b*sb + h*sh + i*st + d
+  int64_t p_sb, p_sh, p_st, s_sb, s_sh, s_st;
+  int64_t B, H, N, P, S;
+  uint16_t *out;                // [B, T, H*64] contiguous
+  int64_t rows;                 // B * T * H
+};
+
+__global__ __launch_bounds__(kThreads) void restore_tokens_kernel(const RestoreParams p) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerWg + (threadIdx.x >> 3);
+  if (row >= p.rows) return;
+  const int sub = threadIdx.x & 7;
+  const int64_t h = row % p.H, bt = row / p.H;
+  const int64_t T = p.N * p.P;
+  const int64_t t = bt % T, b = bt / T;
+  const int64_t n = t / p.P, tf = t % p.P;
+  const uint16_t *src = tf >= p.S
+      ? p.xp + b * p.p_sb + h * p.p_sh + (n * (p.P - p.S) + tf - p.S) * p.p_st
+      : p.xs + b * p.s_sb + h * p.s_sh + (n * p.S + tf) * p.s_st;
+  *reinterpret_cast<u32x4 *>(p.out + (bt * p.H + h) * kHeadDim + sub * 8) =
+      *reinterpret_cast<const u32x4 *>(src + sub * 8);
+}
+
+int check_src(const char *name, const void *ptr, int64_t sb, int64_t st, int64_t sh) {
+  VASC_REQUIRE(ptr != nullptr, "%s is NULL", name);
+  VASC_REQUIRE((reinterpret_cast<uintptr_t>(ptr) & 15) == 0, "%s must be 16-byte aligned", name);
+  VASC_REQUIRE(sb >= 0 && st >= 0 && sh >= 0 && sb % 8 == 0 && st % 8 == 0 && sh % 8 == 0,
+               "%s strides (%lld,%lld,%lld) must be non-negative multiples of 8 elements", name, (long long)sb,
+               (long long)st, (long long)sh);
+  return VASC_OK;
+}
+
+}  // namespace
+}  // namespace vasc
+
+extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int64_t q_sh, const uint16_t *k,
+                             int64_t k_sb, int64_t k_st, int64_t k_sh, const uint16_t *v, int64_t v_sb,
+                             int64_t v_st, int64_t v_sh, int64_t B, int64_t H, int64_t N, int64_t P, int64_t S,
+                             int64_t d, const float *q_norm_w, const float *q_norm_b, float q_eps,
+                             int32_t q_norm, const float *k_norm_w, const float *k_norm_b, float k_eps,
+                             int32_t k_norm, const int32_t *pos, int64_t pos_sb, int64_t pos_st,
+                             const float *rope_cos, const float *rope_sin, int64_t rope_n, uint16_t *q_patch,
+                             uint16_t *q_special, uint16_t *k_out, uint16_t *v_out, void *stream) {
+  using namespace vasc;
+  VASC_SUPPORTED(d == kHeadDim, "head_dim %lld not built (built: 64)", (long long)d);
+  VASC_REQUIRE(B > 0 && H > 0 && N > 0 && P > 0 && S >= 0 && S <= P, "invalid sizes B=%lld H=%lld N=%lld P=%lld S=%lld",
+               (long long)B, (long long)H, (long long)N, (long long)P, (long long)S);
+  int rc;
+  if ((rc = check_src("q", q, q_sb, q_st, q_sh))) return rc;
+  if ((rc = check_src("k", k, k_sb, k_st, k_sh))) return rc;
+  if ((rc = check_src("v", v, v_sb, v_st, v_sh))) return rc;
+  VASC_REQUIRE(k_out && v_out, "k_out and v_out are required");
+  VASC_REQUIRE(P == S || q_patch, "q_patch is required when frames hold patch tokens");
+  VASC_REQUIRE(S == 0 || q_special, "q_special is required when frames hold special tokens");
+  for (const void *o : {static_cast<const void *>(q_patch), static_cast<const void *>(q_special),
+                        static_cast<const void *>(k_out), static_cast<const void *>(v_out)})
+    VASC_REQUIRE((reinterpret_cast<uintptr_t>(o) & 15) == 0, "outputs must be 16-byte aligned");
+  VASC_REQUIRE(q_norm == 0 || q_eps >= 0.f, "q_eps must be non-negative");
+  VASC_REQUIRE(k_norm == 0 || k_eps >= 0.f, "k_eps must be non-negative");
+  if (pos) {
+    VASC_REQUIRE(rope_cos && rope_sin && rope_n > 0, "rotary tables are required with positions");
+    VASC_REQUIRE(pos_sb >= 0 && pos_st >= 2, "position strides must be pos_sb >= 0, pos_st >= 2");
+  }
+  PackParams p;
+  p.src[0] = q; p.src[1] = k; p.src[2] = v;
+  p.sb[0] = q_sb; p.st[0] = q_st; p.sh[0] = q_sh;
+  p.sb[1] = k_sb; p.st[1] = k_st; p.sh[1] = k_sh;
+  p.sb[2] = v_sb; p.st[2] = v_st; p.sh[2] = v_sh;
+  p.B = B; p.H = H; p.N = N; p.P = P; p.S = S;
+  p.norm_w[0] = q_norm_w; p.norm_b[0] = q_norm_b; p.eps[0] = q_eps; p.norm[0] = q_norm;
+  p.norm_w[1] = k_norm_w; p.norm_b[1] = k_norm_b; p.eps[1] = k_eps; p.norm[1] = k_norm;
+  p.pos = pos; p.pos_sb = pos_sb; p.pos_st = pos_st;
+  p.rope_cos = rope_cos; p.rope_sin = rope_sin; p.rope_n = rope_n;
+  p.q_patch = q_patch; p.q_special = q_special; p.k_out = k_out; p.v_out = v_out;
+  p.rows = B * N * P * 3 * H;
+  const int64_t grid = cdiv(p.rows, kRowsPerWg);
+  VASC_REQUIRE(grid < (int64_t(1) << 31), "too many tokens");
+  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  return check_launch("vasc_pack_qkv");
+}
+
+extern "C" int vasc_restore_tokens(const uint16_t *x_patch, int64_t p_sb, int64_t p_sh, int64_t p_st,
+                                   const uint16_t *x_special, int64_t s_sb, int64_t s_sh, int64_t s_st, int64_t B,
+                                   int64_t H, int64_t N, int64_t P, int64_t S, int64_t d, uint16_t *out,
+                                   void *stream) {
+  using namespace vasc;
+  VASC_SUPPORTED(d == kHeadDim, "head_dim %lld not built (built: 64)", (long long)d);
+  VASC_REQUIRE(B > 0 && H > 0 && N > 0 && P > 0 && S >= 0 && S <= P, "invalid sizes");
+  VASC_REQUIRE(out && (reinterpret_cast<uintptr_t>(out) & 15) == 0, "out must be a 16-byte aligned buffer");
+  int rc;
+  if (P > S && (rc = check_src("x_patch", x_patch, p_sb, p_st, p_sh))) return rc;
+  if (S > 0 && (rc = check_src("x_special", x_special, s_sb, s_st, s_sh))) return rc;
+  RestoreParams p;
+  p.xp = x_patch; p.p_sb = p_sb; p.p_sh = p_sh; p.p_st = p_st;
+  p.xs = x_special; p.s_sb = s_sb; p.s_sh = s_sh; p.s_st = s_st;
+  p.B = B; p.H = H; p.N = N; p.P = P; p.S = S;
+  p.out = out;
+  p.rows = B * N * P * H;
+  const int64_t grid = cdiv(p.rows, kRowsPerWg);
+  VASC_REQUIRE(grid < (int64_t(1) << 31), "too many tokens");
+  hipLaunchKernelGGL(restore_tokens_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  return check_launch("vasc_restore_tokens");
+}

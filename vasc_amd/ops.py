@@ -220,3 +220,129 @@ def dense_attn(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, *, scale: flo
     _lib.call("vasc_dense_attn_fwd", q.data_ptr(), *q.stride()[:3], k.data_ptr(), *k.stride()[:3],
               vt.data_ptr(), o.data_ptr(), *o.stride()[:3], B, H, nq, nk, D, float(scale), _stream())
     return o
+
+
+def global_attn(q_patch: torch.Tensor, q_special: torch.Tensor | None, k: torch.Tensor, vt: torch.Tensor,
+                index: torch.Tensor, count: torch.Tensor, *, scale: float | None = None):
+    """Patch queries over their listed blocks and special queries over every
+    key, in one launch. Returns ``(o_patch, o_special or None)`` (bf16)."""
+    q_patch = _bhtd(q_patch, "q_patch")
+    k = _bhtd(k, "k")
+    _dev(vt, "vt")
+    B, H, n_patch, D = q_patch.shape
+    nk = k.shape[2]
+    if vt.shape != (B, H, math.ceil(nk / BLOCK_K), D, BLOCK_K):
+        raise ValueError(f"vt shape {tuple(vt.shape)} does not match K {tuple(k.shape)}")
+    qb = math.ceil(n_patch / BLOCK_Q)
+    index = index.to(torch.int32).contiguous()
+    count = count.to(torch.int32).contiguous()
+    if index.shape[:3] != (B, H, qb) or count.shape != (B, H, qb):
+        raise ValueError(f"index/count must be [B,H,{qb},W]/[B,H,{qb}]")
+    o_patch = torch.empty(B, H, n_patch, D, device=q_patch.device, dtype=torch.bfloat16)
+    n_special = 0
+    o_special = None
+    qs_args = (None, 0, 0, 8)
+    os_args = (None, 0, 0, 8)
+    if q_special is not None and q_special.shape[2] > 0:
+        q_special = _bhtd(q_special, "q_special")
+        n_special = q_special.shape[2]
+        o_special = torch.empty(B, H, n_special, D, device=q_patch.device, dtype=torch.bfloat16)
+        qs_args = (q_special.data_ptr(), *q_special.stride()[:3])
+        os_args = (o_special.data_ptr(), *o_special.stride()[:3])
+    scale = D ** -0.5 if scale is None else scale
+    _lib.call("vasc_global_attn_fwd", q_patch.data_ptr(), *q_patch.stride()[:3], *qs_args, k.data_ptr(),
+              *k.stride()[:3], vt.data_ptr(), o_patch.data_ptr(), *o_patch.stride()[:3], *os_args, B, H, n_patch,
+              n_special, nk, D, index.data_ptr(), index.shape[-1], count.data_ptr(), float(scale), _stream())
+    return o_patch, o_special
+
+
+# ----------------------------------------------------------------- kernel 5
+def _btht(t: torch.Tensor, name: str) -> tuple:
+    """(pointer, sb, st, sh) of a bf16 ``[B,T,H,D]`` view with unit stride on D."""
+    _dev(t, name)
+    if t.dtype != torch.bfloat16 or t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
+        raise ValueError(f"{name} must be bf16 [B,T,H,D] with unit stride on D, 16-byte aligned rows")
+    return t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)
+
+
+def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, frames: int, tokens_per_frame: int,
+             special: int, *, q_norm=None, k_norm=None, pos: torch.Tensor | None = None,
+             rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None):
+    """Frame-major ``[B,T,H,D]`` q/k/v views -> ``(q_patch, q_special, k, v)``
+    in the global layer's ``[patch; special]`` order, ``[B,H,*,D]`` bf16.
+
+    ``q_norm`` / ``k_norm``: ``(weight or None, bias or None, eps)`` of a
+    per-head LayerNorm, or None. ``pos`` int ``[B,T,2]`` (row, column) with
+    ``rope_tables = (cos, sin)`` float32 ``[n, D/4]``: 2D rotary embedding.
+    """
+    B, T, H, D = q.shape
+    N, P, S = int(frames), int(tokens_per_frame), int(special)
+    if N * P != T or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q/k/v must be [B,{N}*{P},H,D], got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    dev = q.device
+    qp = torch.empty(B, H, N * (P - S), D, device=dev, dtype=torch.bfloat16)
+    qs = torch.empty(B, H, N * S, D, device=dev, dtype=torch.bfloat16)
+    ko = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+    vo = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+    keep = []
+
+    def norm_args(nrm, name):
+        if nrm is None:
+            return (None, None, 0.0, 0)
+        w, b, eps = nrm
+        out = []
+        for t in (w, b):
+            if t is None:
+                out.append(None)
+            else:
+                t = t.detach().float().contiguous()
+                if t.numel() != D:
+                    raise ValueError(f"{name} parameters must hold {D} values")
+                _dev(t, name)
+                keep.append(t)
+                out.append(t.data_ptr())
+        return (out[0], out[1], float(eps), 1)
+
+    rope = (None, 0, 2, None, None, 0)
+    if pos is not None:
+        if rope_tables is None:
+            raise ValueError("rope_tables are required with pos")
+        _dev(pos, "pos")
+        pos32 = pos.to(torch.int32)
+        if pos32.dim() == 2:
+            pos32 = pos32.unsqueeze(0)
+        if pos32.shape[-2:] != (T, 2) or pos32.stride(-1) != 1:
+            pos32 = pos32.reshape(-1, T, 2).contiguous()
+        if pos32.dim() != 3 or pos32.shape[0] not in (1, B):
+            raise ValueError(f"pos must be [{B} or 1, {T}, 2], got {tuple(pos.shape)}")
+        cos, sin = (t.float().contiguous() for t in rope_tables)
+        if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D // 4:
+            raise ValueError(f"rope tables must be [n, {D // 4}]")
+        keep += [pos32, cos, sin]
+        rope = (pos32.data_ptr(), pos32.stride(0) if pos32.shape[0] > 1 else 0, pos32.stride(1), cos.data_ptr(),
+                sin.data_ptr(), cos.shape[0])
+    qn, kn = norm_args(q_norm, "q_norm"), norm_args(k_norm, "k_norm")
+    _lib.call("vasc_pack_qkv", *_btht(q, "q"), *_btht(k, "k"), *_btht(v, "v"), B, H, N, P, S, D,
+              qn[0], qn[1], qn[2], qn[3], kn[0], kn[1], kn[2], kn[3], *rope,
+              qp.data_ptr(), qs.data_ptr(), ko.data_ptr(), vo.data_ptr(), _stream())
+    return qp, (qs if S else None), ko, vo
+
+
+def restore_tokens(x_patch: torch.Tensor, x_special: torch.Tensor | None, frames: int, tokens_per_frame: int,
+                   special: int) -> torch.Tensor:
+    """``[B,H,Np,D]`` + ``[B,H,Ns,D]`` -> frame-major ``[B,T,H*D]`` (bf16)."""
+    x_patch = _bhtd(x_patch, "x_patch")
+    B, H, n_patch, D = x_patch.shape
+    N, P, S = int(frames), int(tokens_per_frame), int(special)
+    if n_patch != N * (P - S):
+        raise ValueError(f"x_patch holds {n_patch} tokens, expected {N * (P - S)}")
+    xs = (None, 0, 0, 8)
+    if S:
+        if x_special is None or x_special.shape[2] != N * S:
+            raise ValueError(f"x_special must hold {N * S} tokens")
+        x_special = _bhtd(x_special, "x_special")
+        xs = (x_special.data_ptr(), *x_special.stride()[:3])
+    out = torch.empty(B, N * P, H * D, device=x_patch.device, dtype=torch.bfloat16)
+    _lib.call("vasc_restore_tokens", x_patch.data_ptr(), *x_patch.stride()[:3], *xs, B, H, N, P, S, D,
+              out.data_ptr(), _stream())
+    return out

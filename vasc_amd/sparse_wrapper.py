@@ -287,26 +287,16 @@ def _check_research_kwargs(kwargs: dict) -> None:
             raise TypeError(f"block_sparse_attn_cuda() got an unexpected keyword argument {name!r}")
 
 
-def block_sparse_attn_cuda(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                           pooled_score: torch.Tensor, topk: int | None = None, sparse_ratio: float | None = None,
-                           cdf_threshold: float | None = None, return_sparsity: bool = False,
-                           dtype: torch.dtype = torch.float16, *, layer_idx: int = 0,
-                           routing_stats_store: dict | None = None, routing_state: dict | None = None,
-                           num_patch_tokens: int | None = None, **research):
-    """Sparse global attention of the patch queries (SW:6868-8245).
-
-    query ``[B,H,Nq,D]`` (patch queries), key/value ``[B,H,Tk,D]`` with the
-    special tokens appended, pooled_score ``[B,H,ceil(Nq/128),ceil(Np/64)]``.
-    The selection mode follows the reference's ``SPARSE_VGGT_*`` switches
-    (``vasc`` when ``COSA_VALUE_RISK_PAIR_DEBT`` is on, else ``topk``).
-    ``dtype`` is accepted for signature compatibility: the kernel computes
-    in bf16. Returns ``o`` (query dtype) or ``(o, sparsity)``.
-    """
+def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torch.Tensor, topk, sparse_ratio,
+                      cdf_threshold, layer_idx: int, routing_stats_store, routing_state, num_patch_tokens,
+                      research: dict):
+    """Mode switch, budget, mixed-tail and sink rules and kernel 2 of
+    block_sparse_attn_cuda (SW:6998-7041, 7559-7770). Returns the selection
+    and the total key-block count."""
     _check_research_kwargs(research)
-    for t, name in ((query, "query"), (key, "key"), (value, "value"), (pooled_score, "pooled_score")):
+    for t, name in ((key, "key"), (value, "value"), (pooled_score, "pooled_score")):
         _require_gpu(t, name)
     cfg = routing_config()
-    out_dtype = query.dtype
     Tk = key.shape[-2]
     orig_kblk = pooled_score.shape[-1]
     total_kblk = math.ceil(Tk / KBLK)
@@ -338,12 +328,55 @@ def block_sparse_attn_cuda(query: torch.Tensor, key: torch.Tensor, value: torch.
     else:
         sel = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=t, force_last=force_last,
                                 sink_blocks=sink)
+    return sel, total_kblk
+
+
+def _sparsity(sel: dict, total_kblk: int) -> torch.Tensor:
+    """``1 - mean(final_map)`` over the patch and sink columns (SW:8218-8245)."""
+    kept = sel["count"].sum(dtype=torch.float64)
+    return (1.0 - kept / float(sel["count"].numel() * total_kblk)).float()
+
+
+def block_sparse_attn_cuda(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                           pooled_score: torch.Tensor, topk: int | None = None, sparse_ratio: float | None = None,
+                           cdf_threshold: float | None = None, return_sparsity: bool = False,
+                           dtype: torch.dtype = torch.float16, *, layer_idx: int = 0,
+                           routing_stats_store: dict | None = None, routing_state: dict | None = None,
+                           num_patch_tokens: int | None = None, **research):
+    """Sparse global attention of the patch queries (SW:6868-8245).
+
+    query ``[B,H,Nq,D]`` (patch queries), key/value ``[B,H,Tk,D]`` with the
+    special tokens appended, pooled_score ``[B,H,ceil(Nq/128),ceil(Np/64)]``.
+    The selection mode follows the reference's ``SPARSE_VGGT_*`` switches
+    (``vasc`` when ``COSA_VALUE_RISK_PAIR_DEBT`` is on, else ``topk``).
+    ``dtype`` is accepted for signature compatibility: the kernel computes
+    in bf16. Returns ``o`` (query dtype) or ``(o, sparsity)``.
+    """
+    _require_gpu(query, "query")
+    sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
+                                        routing_stats_store, routing_state, num_patch_tokens, research)
     vt = ops.pack_v(value)
     o = ops.block_sparse_attn(query, key, vt, sel["index"], sel["count"])
-    if o.dtype != out_dtype:
-        o = o.to(out_dtype)
+    if o.dtype != query.dtype:
+        o = o.to(query.dtype)
     if return_sparsity:
-        kept = sel["count"].sum(dtype=torch.float64)
-        sparsity = (1.0 - kept / float(sel["count"].numel() * total_kblk)).float()
-        return o, sparsity
+        return o, _sparsity(sel, total_kblk)
     return o
+
+
+def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | None, key: torch.Tensor,
+                            value: torch.Tensor, pooled_score: torch.Tensor, *, sparse_ratio: float | None = None,
+                            topk: int | None = None, cdf_threshold: float | None = None, layer_idx: int = 0,
+                            routing_stats_store: dict | None = None, routing_state: dict | None = None,
+                            num_patch_tokens: int | None = None, **research):
+    """``block_sparse_attn_cuda`` for a whole global layer: the selection of
+    the patch queries as there, and the special-token queries (which the
+    reference runs through a dense SDPA, ATT:8464-8484) over every key in
+    the same attention launch. Returns ``(o_patch, o_special, sparsity)``
+    in bf16 (``o_special`` None without special queries)."""
+    _require_gpu(q_patch, "query")
+    sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
+                                        routing_stats_store, routing_state, num_patch_tokens, research)
+    vt = ops.pack_v(value)
+    o_patch, o_special = ops.global_attn(q_patch, q_special, key, vt, sel["index"], sel["count"])
+    return o_patch, o_special, _sparsity(sel, total_kblk)
