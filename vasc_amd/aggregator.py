@@ -15,6 +15,12 @@ provides modules of the same shape for the benchmarks and tests:
   ``k_norm`` (LayerNorm), ``rope``, ``proj`` and ``proj_drop``, the fields
   ``adaptive_sparse_attention_forward`` reads. Its own ``forward`` is the
   dense layer on this build's MFMA attention kernel.
+* ``Block`` (pre-norm attention + MLP with LayerScale), ``Aggregator``
+  (VGGT: 24 frame / 24 global blocks, 1 camera + 4 register tokens per
+  frame, readouts at layers 4, 11, 17, 23; vggt.py:64-212) and
+  ``Pi3Decoder`` (36 blocks, odd ones global, 5 register tokens;
+  pi3.py:70-135). The upstream DINOv2 patch embedding is replaced by one
+  14x14 convolution. ``vasc_amd.install`` patches their global blocks.
 """
 from __future__ import annotations
 
@@ -118,3 +124,168 @@ def fused_layout_supported(attn: nn.Module) -> bool:
         return False
     rope = getattr(attn, "rope", None)
     return rope is None or isinstance(rope, RotaryPositionEmbedding2D)
+
+
+class Mlp(nn.Module):
+    def __init__(self, dim: int, hidden: int):
+        super().__init__()
+        self.fc1 = nn.Linear(dim, hidden)
+        self.act = nn.GELU()
+        self.fc2 = nn.Linear(hidden, dim)
+
+    def forward(self, x):
+        return self.fc2(self.act(self.fc1(x)))
+
+
+class LayerScale(nn.Module):
+    def __init__(self, dim: int, init_values: float = 0.01):
+        super().__init__()
+        self.gamma = nn.Parameter(torch.full((dim,), float(init_values)))
+
+    def forward(self, x):
+        return x * self.gamma
+
+
+class Block(nn.Module):
+    """Pre-norm transformer block: ``x + ls1(attn(norm1(x))) + ls2(mlp(norm2(.)))``."""
+
+    def __init__(self, dim: int = 1024, num_heads: int = 16, mlp_ratio: float = 4.0,
+                 rope: RotaryPositionEmbedding2D | None = None, init_values: float = 0.01):
+        super().__init__()
+        self.norm1 = nn.LayerNorm(dim, eps=1e-6)
+        self.attn = Attention(dim, num_heads, rope=rope)
+        self.ls1 = LayerScale(dim, init_values)
+        self.norm2 = nn.LayerNorm(dim, eps=1e-6)
+        self.mlp = Mlp(dim, int(dim * mlp_ratio))
+        self.ls2 = LayerScale(dim, init_values)
+
+    def forward(self, x: torch.Tensor, pos: torch.Tensor | None = None) -> torch.Tensor:
+        x = x + self.ls1(self.attn(self.norm1(x), pos=pos))
+        return x + self.ls2(self.mlp(self.norm2(x)))
+
+
+def grid_positions(frames: int, h: int, w: int, special: int, device) -> torch.Tensor:
+    """``[frames, special + h*w, 2]`` integer (row, column) positions: patch
+    tokens get ``(y+1, x+1)``, special tokens ``(0, 0)`` (vggt.py:122-131)."""
+    ys, xs = torch.meshgrid(torch.arange(h, device=device), torch.arange(w, device=device), indexing="ij")
+    patch = torch.stack([ys.reshape(-1), xs.reshape(-1)], -1) + 1
+    pos = torch.cat([torch.zeros(special, 2, dtype=patch.dtype, device=device), patch])
+    return pos.unsqueeze(0).expand(frames, -1, -1)
+
+
+class Aggregator(nn.Module):
+    """VGGT-shaped alternating frame/global attention aggregator.
+
+    The upstream patch embedding is a DINOv2 ViT; here it is one 14x14
+    convolution (the benchmark measures the attention blocks). Tokens per
+    frame: 1 camera + ``num_register_tokens`` registers + the patches; the
+    first frame uses its own camera/register tokens (slice_expand_and_flatten).
+    Frame blocks attend inside each frame, global blocks across all frames.
+    """
+
+    def __init__(self, dim: int = 1024, depth: int = 24, num_heads: int = 16, mlp_ratio: float = 4.0,
+                 patch_size: int = 14, num_register_tokens: int = 4, camera_token: bool = True,
+                 intermediate_layer_idx=(4, 11, 17, 23)):
+        super().__init__()
+        self.patch_size = patch_size
+        self.patch_embed = nn.Conv2d(3, dim, patch_size, patch_size)
+        self.rope = RotaryPositionEmbedding2D(100.0)
+        self.frame_blocks = nn.ModuleList([Block(dim, num_heads, mlp_ratio, self.rope) for _ in range(depth)])
+        self.global_blocks = nn.ModuleList([Block(dim, num_heads, mlp_ratio, self.rope) for _ in range(depth)])
+        self.camera_token = nn.Parameter(torch.randn(1, 2, 1, dim) * 1e-6) if camera_token else None
+        self.register_token = nn.Parameter(torch.randn(1, 2, num_register_tokens, dim) * 1e-6)
+        self.patch_start_idx = int(camera_token) + num_register_tokens
+        self.aa_block_num = depth
+        self.intermediate_layer_idx = list(intermediate_layer_idx)
+        self.register_buffer("_resnet_mean", torch.tensor([0.485, 0.456, 0.406]).view(1, 1, 3, 1, 1), persistent=False)
+        self.register_buffer("_resnet_std", torch.tensor([0.229, 0.224, 0.225]).view(1, 1, 3, 1, 1), persistent=False)
+
+    @staticmethod
+    def _expand(token: torch.Tensor, B: int, N: int) -> torch.Tensor:
+        first = token[:, :1].expand(B, 1, *token.shape[2:])
+        rest = token[:, 1:].expand(B, N - 1, *token.shape[2:])
+        return torch.cat([first, rest], dim=1).reshape(B * N, *token.shape[2:])
+
+    def forward(self, images: torch.Tensor):
+        """images ``[B, N, 3, H, W]`` in [0, 1] -> (list of per-layer outputs, patch_start_idx)."""
+        routing_state = getattr(self, "_sparse_routing_state", None)
+        if routing_state is not None:
+            routing_state.clear()
+        B, N, _, Hi, Wi = images.shape
+        x = ((images - self._resnet_mean) / self._resnet_std).view(B * N, 3, Hi, Wi).to(self.patch_embed.weight.dtype)
+        tokens = self.patch_embed(x).flatten(2).transpose(1, 2)
+        special = [self._expand(self.register_token, B, N)]
+        if self.camera_token is not None:
+            special.insert(0, self._expand(self.camera_token, B, N))
+        tokens = torch.cat([*(s.to(tokens.dtype) for s in special), tokens], dim=1)
+        h, w = Hi // self.patch_size, Wi // self.patch_size
+        P, C = tokens.shape[1], tokens.shape[2]
+        pos = grid_positions(B * N, h, w, self.patch_start_idx, images.device)
+        outputs = []
+        for i in range(self.aa_block_num):
+            tokens = self.frame_blocks[i](tokens.view(B * N, P, C), pos=pos)
+            frame_out = tokens.view(B, N, P, C)
+            tokens = self.global_blocks[i](tokens.view(B, N * P, C), pos=pos.reshape(B, N * P, 2))
+            if i in self.intermediate_layer_idx:
+                outputs.append(torch.cat([frame_out, tokens.view(B, N, P, C)], dim=-1))
+            else:
+                outputs.append(None)
+        _finalize(self)
+        return outputs, self.patch_start_idx
+
+
+class Pi3Decoder(nn.Module):
+    """Pi3-shaped decoder: alternating frame (even) / global (odd) blocks over
+    5 register tokens + the patch tokens of each frame (pi3.py:70-135)."""
+
+    def __init__(self, dim: int = 1024, depth: int = 36, num_heads: int = 16, mlp_ratio: float = 4.0,
+                 patch_size: int = 14, num_register_tokens: int = 5):
+        super().__init__()
+        self.patch_size = patch_size
+        self.patch_embed = nn.Conv2d(3, dim, patch_size, patch_size)
+        self.rope = RotaryPositionEmbedding2D(100.0)
+        self.decoder = nn.ModuleList([Block(dim, num_heads, mlp_ratio, self.rope) for _ in range(depth)])
+        self.register_token = nn.Parameter(torch.randn(1, 1, num_register_tokens, dim) * 1e-6)
+        self.patch_start_idx = num_register_tokens
+
+    def forward(self, images: torch.Tensor):
+        """images ``[B, N, 3, H, W]`` -> (concatenated last two outputs, positions)."""
+        B, N, _, Hi, Wi = images.shape
+        x = images.view(B * N, 3, Hi, Wi).to(self.patch_embed.weight.dtype)
+        hidden = self.patch_embed(x).flatten(2).transpose(1, 2)
+        return self.decode(hidden, N, Hi, Wi)
+
+    def decode(self, hidden: torch.Tensor, N: int, H: int, W: int):
+        routing_state = getattr(self, "_sparse_routing_state", None)
+        if routing_state is not None:
+            routing_state.clear()
+        BN, hw, C = hidden.shape
+        B = BN // N
+        reg = self.register_token.repeat(B, N, 1, 1).reshape(B * N, *self.register_token.shape[-2:])
+        hidden = torch.cat([reg.to(hidden.dtype), hidden], dim=1)
+        hw = hidden.shape[1]
+        pos = grid_positions(B * N, H // self.patch_size, W // self.patch_size, self.patch_start_idx, hidden.device)
+        final = []
+        for i, blk in enumerate(self.decoder):
+            if i % 2 == 0:
+                hidden = blk(hidden.reshape(B * N, hw, C), pos=pos.reshape(B * N, hw, 2))
+            else:
+                hidden = blk(hidden.reshape(B, N * hw, C), pos=pos.reshape(B, N * hw, 2))
+            if i + 1 in (len(self.decoder) - 1, len(self.decoder)):
+                final.append(hidden.reshape(B * N, hw, C))
+        _finalize(self)
+        return torch.cat(final, dim=-1), pos
+
+
+def _finalize(model: nn.Module) -> None:
+    """Terminal ledger settlement after the last layer (vggt.py:193-204, pi3.py:23-36)."""
+    routing_state = getattr(model, "_sparse_routing_state", None)
+    if routing_state is None:
+        return
+    from .sparse_wrapper import finalize_cosa_value_risk_pair_debt
+    store = getattr(model, "_sparse_aux_output_store", None)
+    stats = None
+    if store:
+        last = store[max(store)]
+        stats = last if isinstance(last, dict) else None
+    finalize_cosa_value_risk_pair_debt(routing_state, stats_store=stats)
