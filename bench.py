@@ -244,6 +244,79 @@ def run_c5(dev) -> int:
     return 0
 
 
+def run_aggregator(dev, frames: int, ratios, reps: int = 5, warmup: int = 2) -> dict:
+    """C2's VGGT-shaped aggregator (24 frame + 24 global blocks, dim 1024, 16
+    heads, MLP 4096, random init bf16) on seeded uniform-noise images
+    ``[1, frames, 3, 392, 518]``: dense (every global block on the dense MFMA
+    kernel) and vasc with the structural profile. Reports the forward time
+    (frames/s = frames / forward seconds) and, as the reference's
+    CudaAttentionTimer does (eval_7scenes_sparse_vggt.py:1533-1574), hipEvents
+    around every global attention module (qkv, layout, sparse op, restore,
+    proj), summed per forward."""
+    from vasc_amd import install
+    from vasc_amd.aggregator import Aggregator
+    from vasc_amd.launcher import method_environment
+
+    torch.manual_seed(0)
+    with torch.device(dev):
+        agg = Aggregator(dim=1024, depth=24, num_heads=16, mlp_ratio=4.0)
+    agg = agg.to(torch.bfloat16).eval()
+    g = torch.Generator(device=dev).manual_seed(0)
+    images = torch.rand(1, frames, 3, 392, 518, device=dev, generator=g)
+    events: list = []
+
+    def pre(mod, args, kwargs=None):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        events.append([ev, None])
+
+    def post(mod, args, out):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        events[-1][1] = ev
+
+    for blk in agg.global_blocks:
+        blk.attn.register_forward_pre_hook(pre)
+        blk.attn.register_forward_hook(post)
+
+    def measure(tag):
+        fwd, attn = [], []
+        with torch.no_grad():
+            for i in range(warmup + reps):
+                events.clear()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                agg(images)
+                b.record()
+                torch.cuda.synchronize()
+                if i >= warmup:
+                    fwd.append(a.elapsed_time(b))
+                    attn.append(sum(x.elapsed_time(y) for x, y in events))
+        f, t = statistics.median(fwd), statistics.median(attn)
+        log(f"aggregator {tag}: forward {f:.2f} ms ({frames / (f * 1e-3):.1f} frames/s), "
+            f"24 global attention layers {t:.2f} ms ({t / len(agg.global_blocks):.3f} ms/layer)")
+        return {"forward_ms": f, "frames_per_s": frames / (f * 1e-3), "global_attn_ms_per_forward": t,
+                "global_layer_ms": t / len(agg.global_blocks), "frames_per_s_global_layers": frames / (t * 1e-3)}
+
+    out = {"dense": measure("dense")}
+    saved = {k: os.environ.pop(k) for k in list(os.environ) if k.startswith("SPARSE_VGGT_")}
+    os.environ.update(method_environment("vggt", "vasc"))
+    try:
+        install.sparse_aggregator_from_vggt_layerwise(agg, layer_sparsity_ratios=ratios, verbose=False)
+        out["vasc"] = measure("vasc")
+    finally:
+        for k in [k for k in os.environ if k.startswith("SPARSE_VGGT_")]:
+            del os.environ[k]
+        os.environ.update(saved)
+    out["speedup_global_layers_vs_dense"] = out["dense"]["global_attn_ms_per_forward"] / \
+        out["vasc"]["global_attn_ms_per_forward"]
+    out["config"] = ("VGGT-shaped aggregator, random-init bf16, 14x14 conv patch embedding, "
+                     f"{frames} frames of 392x518 uniform noise, vasc with the structural profile")
+    del agg
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(layer, ratio, frames, n_layers):
     from oracle import cpu_baseline as cb
     cores = len(os.sched_getaffinity(0))
@@ -277,6 +350,8 @@ def main() -> int:
     ap.add_argument("--sparsity", type=float, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-aggregator", action="store_true",
+                    help="skip the VGGT-shaped aggregator forward (global-layer ms in the reference's timer scope)")
     ap.add_argument("--graph", dest="graph", action="store_true", default=True,
                     help="replay the step as a HIP graph (default)")
     ap.add_argument("--no-graph", dest="graph", action="store_false")
@@ -454,8 +529,18 @@ def main() -> int:
         result["speedup_vs_dense"] = dense_ms / layer_ms
         log(f"dense attention {dense_ms:.3f} ms/layer ({result['dense_tflops']:.1f} TFLOP/s)")
 
+    if not args.no_aggregator and args.workload == "c2":
+        del layers
+        torch.cuda.empty_cache()
+        result["aggregator"] = run_aggregator(dev, N, ratios)
+        result["global_layer_ms"] = result["aggregator"]["vasc"]["global_layer_ms"]
+
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(layers[0], ratios[0], N, L)
+        if args.no_aggregator or args.workload != "c2":
+            q0, k0, v0 = layers[0]
+        else:
+            q0, k0, v0 = synthetic_layer(N, P, S, H, D, seed=0, device=dev)
+        result["cpu_baseline"] = cpu_baseline((q0, k0, v0), ratios[0], N, L)
         log(f"cpu baseline {result['cpu_baseline']['layer_s']:.2f} s/layer")
 
     print(json.dumps(result), flush=True)
