@@ -243,7 +243,8 @@ int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
  *     out_j      = x_j cos(a) - x_{j+d/4} sin(a)
  *     out_{j+d/4} = x_{j+d/4} cos(a) + x_j sin(a),   a = position * freq_j
  *   with cos/sin read from rope_cos / rope_sin [rope_n, d/4] (float32,
- *   entry (position, j)); positions are clamped into [0, rope_n).
+ *   entry (position, j), 16-byte aligned); positions are clamped into
+ *   [0, rope_n).
  * Outputs (contiguous bf16): q_patch [B,H,N*(P-S),d], q_special [B,H,N*S,d],
  *   k_out / v_out [B,H,T,d] with the patch tokens of all frames first, then
  *   the special tokens. Arithmetic in float32, one bf16 rounding per output.

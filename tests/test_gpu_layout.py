@@ -70,7 +70,7 @@ def test_pack_norm_and_rotary():
     ys, xs = torch.meshgrid(torch.arange(Hp), torch.arange(Wp), indexing="ij")
     frame_pos = torch.cat([torch.zeros(S, 2, dtype=torch.long), torch.stack([ys.reshape(-1), xs.reshape(-1)], -1) + 1])
     pos = frame_pos.repeat(N, 1)  # [T, 2]
-    cos, sin = RotaryPositionEmbedding2D().tables(int(pos.max()) + 1, D, "cuda")
+    cos, sin = RotaryPositionEmbedding2D().tables(D, "cuda")
     x = qkv.cuda().view(1, N * P, 3, H, D)
     qp, qs, k, v = ops.pack_qkv(x[:, :, 0], x[:, :, 1], x[:, :, 2], N, P, S, q_norm=(qw.cuda(), qb.cuda(), 1e-6),
                                 k_norm=(kw.cuda(), None, 1e-5), pos=pos.cuda(), rope_tables=(cos, sin))
@@ -156,7 +156,7 @@ def test_global_layer_sparse_matches_oracle_layer():
             out = adaptive_sparse_attention_forward(m, x, pos, sparse_ratio=0.5, num_special_tokens=S,
                                                     num_heads=heads, routing_state={})
             qkv = m.qkv(x)
-            cos, sin = m.rope.tables(int(pos.max()) + 1, dim // heads, "cuda")
+            cos, sin = m.rope.tables(dim // heads, "cuda")
             qp, qsp, kre, vre = OL.pack_layer(
                 qkv.float().cpu().numpy(), N, P, S, heads,
                 q_norm=(m.q_norm.weight.float().cpu().numpy(), m.q_norm.bias.float().cpu().numpy(), m.q_norm.eps),

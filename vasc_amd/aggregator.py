@@ -30,25 +30,33 @@ import torch
 from torch import nn
 
 from . import ops
+from .attention import frame_grid
 
 
 class RotaryPositionEmbedding2D(nn.Module):
-    """2D rotary position embedding with host-computed cos/sin tables."""
+    """2D rotary position embedding with host-computed cos/sin tables.
+
+    The tables cover positions ``[0, MAX_POSITIONS)`` (a grid of up to 4096
+    patches per side); larger positions are clamped to the last entry, by
+    the layout kernel and by ``forward`` alike, so no call has to read the
+    positions back to size the tables.
+    """
+
+    MAX_POSITIONS = 4096
 
     def __init__(self, frequency: float = 100.0):
         super().__init__()
         self.base_frequency = float(frequency)
         self._tables: dict = {}
 
-    def tables(self, n_positions: int, head_dim: int, device) -> tuple[torch.Tensor, torch.Tensor]:
-        """float32 ``(cos, sin)`` of ``p * base**(-2j/(head_dim/2))``, shape ``[n, head_dim/4]``."""
-        n = max(int(n_positions), 1)
+    def tables(self, head_dim: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+        """float32 ``(cos, sin)`` of ``p * base**(-2j/(head_dim/2))``, shape ``[MAX_POSITIONS, head_dim/4]``."""
         key = (head_dim, str(device))
         have = self._tables.get(key)
-        if have is None or have[0].shape[0] < n:
+        if have is None:
             half = head_dim // 2
             inv = 1.0 / (self.base_frequency ** (torch.arange(0, half, 2, dtype=torch.float64) / half))
-            ang = torch.arange(n, dtype=torch.float64)[:, None] * inv[None, :]
+            ang = torch.arange(self.MAX_POSITIONS, dtype=torch.float64)[:, None] * inv[None, :]
             have = (ang.cos().float().to(device), ang.sin().float().to(device))
             self._tables[key] = have
         return have
@@ -57,11 +65,11 @@ class RotaryPositionEmbedding2D(nn.Module):
         """tokens ``[B,H,T,D]``, positions ``[B,T,2]`` integer (row, column)."""
         D = tokens.shape[-1]
         q4 = D // 4
-        cos, sin = self.tables(int(positions.max()) + 1, D, tokens.device)
+        cos, sin = self.tables(D, tokens.device)
         x = tokens.float()
         out = torch.empty_like(x)
         for half in range(2):
-            p = positions[..., half].long()
+            p = positions[..., half].long().clamp(0, self.MAX_POSITIONS - 1)
             c, s = cos[p][:, None], sin[p][:, None]  # [B,1,T,D/4]
             lo = x[..., half * 2 * q4: half * 2 * q4 + q4]
             hi = x[..., half * 2 * q4 + q4: (half + 1) * 2 * q4]
@@ -101,7 +109,7 @@ class Attention(nn.Module):
     def _tables(self, pos, head_dim, device):
         if self.rope is None or pos is None:
             return None
-        return self.rope.tables(int(pos.max()) + 1, head_dim, device)
+        return self.rope.tables(head_dim, device)
 
 
 def layer_norm_args(norm: nn.Module):
@@ -222,14 +230,15 @@ class Aggregator(nn.Module):
         P, C = tokens.shape[1], tokens.shape[2]
         pos = grid_positions(B * N, h, w, self.patch_start_idx, images.device)
         outputs = []
-        for i in range(self.aa_block_num):
-            tokens = self.frame_blocks[i](tokens.view(B * N, P, C), pos=pos)
-            frame_out = tokens.view(B, N, P, C)
-            tokens = self.global_blocks[i](tokens.view(B, N * P, C), pos=pos.reshape(B, N * P, 2))
-            if i in self.intermediate_layer_idx:
-                outputs.append(torch.cat([frame_out, tokens.view(B, N, P, C)], dim=-1))
-            else:
-                outputs.append(None)
+        with frame_grid(h, w):
+            for i in range(self.aa_block_num):
+                tokens = self.frame_blocks[i](tokens.view(B * N, P, C), pos=pos)
+                frame_out = tokens.view(B, N, P, C)
+                tokens = self.global_blocks[i](tokens.view(B, N * P, C), pos=pos.reshape(B, N * P, 2))
+                if i in self.intermediate_layer_idx:
+                    outputs.append(torch.cat([frame_out, tokens.view(B, N, P, C)], dim=-1))
+                else:
+                    outputs.append(None)
         _finalize(self)
         return outputs, self.patch_start_idx
 
@@ -264,15 +273,17 @@ class Pi3Decoder(nn.Module):
         reg = self.register_token.repeat(B, N, 1, 1).reshape(B * N, *self.register_token.shape[-2:])
         hidden = torch.cat([reg.to(hidden.dtype), hidden], dim=1)
         hw = hidden.shape[1]
-        pos = grid_positions(B * N, H // self.patch_size, W // self.patch_size, self.patch_start_idx, hidden.device)
+        h, w = H // self.patch_size, W // self.patch_size
+        pos = grid_positions(B * N, h, w, self.patch_start_idx, hidden.device)
         final = []
-        for i, blk in enumerate(self.decoder):
-            if i % 2 == 0:
-                hidden = blk(hidden.reshape(B * N, hw, C), pos=pos.reshape(B * N, hw, 2))
-            else:
-                hidden = blk(hidden.reshape(B, N * hw, C), pos=pos.reshape(B, N * hw, 2))
-            if i + 1 in (len(self.decoder) - 1, len(self.decoder)):
-                final.append(hidden.reshape(B * N, hw, C))
+        with frame_grid(h, w):
+            for i, blk in enumerate(self.decoder):
+                if i % 2 == 0:
+                    hidden = blk(hidden.reshape(B * N, hw, C), pos=pos.reshape(B * N, hw, 2))
+                else:
+                    hidden = blk(hidden.reshape(B, N * hw, C), pos=pos.reshape(B, N * hw, 2))
+                if i + 1 in (len(self.decoder) - 1, len(self.decoder)):
+                    final.append(hidden.reshape(B * N, hw, C))
         _finalize(self)
         return torch.cat(final, dim=-1), pos
 

@@ -11,6 +11,8 @@ Mirrors ``src/sparse_vggt/models/attention.py`` (``ATT``) of the reference:
 """
 from __future__ import annotations
 
+import contextlib
+import contextvars
 import math
 
 import torch
@@ -37,11 +39,33 @@ def predict_attention(query: torch.Tensor, key: torch.Tensor, ks_q: int = 128, k
     return ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(query.shape[-1]))
 
 
+_FRAME_GRID: contextvars.ContextVar = contextvars.ContextVar("vasc_frame_grid", default=None)
+
+
+@contextlib.contextmanager
+def frame_grid(h: int, w: int):
+    """Announce the patch grid of the frames for the layers run inside.
+
+    The layer forward otherwise reads the grid back from the positions
+    (ATT:8343-8349), a device-to-host copy in every layer; model forwards
+    that built the positions themselves pass the grid here instead.
+    """
+    token = _FRAME_GRID.set((int(h), int(w)))
+    try:
+        yield
+    finally:
+        _FRAME_GRID.reset(token)
+
+
 def _infer_frames(pos: torch.Tensor, n_tokens: int, S: int):
     """H, W, N, P from the RoPE positions (ATT:8343-8349): patch positions are
     1-based (specials sit at 0), so the maxima are the grid sizes."""
-    H = int(pos[0].max(0).values[0])
-    W = int(pos[0].max(0).values[1])
+    grid = _FRAME_GRID.get()
+    if grid is not None:
+        H, W = grid
+    else:
+        H = int(pos[0].max(0).values[0])
+        W = int(pos[0].max(0).values[1])
     P = H * W + S
     N = n_tokens // P
     assert N * P == n_tokens, f"{N=}, {H=}, {W=}, {S=}, {n_tokens=}"
@@ -77,7 +101,7 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
     qkv = self.qkv(x).to(torch.bfloat16).view(B, NP, 3, nh, hd)
     rope = getattr(self, "rope", None)
     if fused_layout_supported(self):
-        tables = rope.tables(int(pos.max()) + 1, hd, x.device) if rope is not None else None
+        tables = rope.tables(hd, x.device) if rope is not None else None
         q_patch, q_special, k_re, v_re = ops.pack_qkv(
             qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], N, P, S, q_norm=layer_norm_args(self.q_norm),
             k_norm=layer_norm_args(self.k_norm), pos=pos if rope is not None else None, rope_tables=tables)

@@ -19,7 +19,10 @@
 // Eight lanes own one (token, tensor, head) row of 64 features, 8 per lane,
 // so a row is one 128-byte segment on both sides; the LayerNorm sums are
 // xor butterflies inside the 8-lane group and the rotary partner of a
-// feature (16 places away inside its half) sits two lanes away.
+// feature (16 places away inside its half) sits two lanes away. A
+// workgroup takes 64 tokens of one tensor and head (index arithmetic in 32
+// bits, tensor and head scalar), and issues both of a lane's loads before
+// it uses the first.
 // Precedent in the reference: kernels/qkv_layout.py:8-157 (layout only).
 #include "common.h"
 
@@ -28,122 +31,174 @@ namespace {
 
 constexpr int kHeadDim = 64;
 constexpr int kThreads = 256;
-constexpr int kRowsPerWg = kThreads / 8;
+constexpr int kRows = kThreads / 8;  // token rows per pass: 8 lanes per 64-feature row
+constexpr int kPasses = 2;           // token rows per lane group
+constexpr int kTokens = kRows * kPasses;
 
 struct PackParams {
   const uint16_t *src[3];       // q, k, v: element (b, t, h, d) at src + b*sb + t*st + h*sh + d
   int64_t sb[3], st[3], sh[3];
-  int64_t B, H, N, P, S;        // T = N * P frame-major tokens
+  int32_t H, N, P, S;           // T = N * P frame-major tokens
   const float *norm_w[2], *norm_b[2];
   float eps[2];
   int32_t norm[2];              // LayerNorm of q (0) and k (1)
   const int32_t *pos;           // (row, column) position of token (b, t) at pos + b*pos_sb + t*pos_st
   int64_t pos_sb, pos_st;
   const float *rope_cos, *rope_sin;  // [rope_n, 16]: cos/sin of position p times frequency i
-  int64_t rope_n;
+  int32_t rope_n;
   uint16_t *q_patch, *q_special, *k_out, *v_out;
-  int64_t rows;                 // B * T * 3 * H
 };
 
+// Cross-lane moves inside groups of 8 lanes by DPP: xor 1 and xor 2 are
+// quad permutations, and the half-row mirror (lane i <-> 7 - i) reaches the
+// other quad of the group.
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+constexpr int kQuadXor1 = 0xb1;   // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4e;   // quad_perm [2, 3, 0, 1]
+constexpr int kHalfMirror = 0x141;
+
 __device__ __forceinline__ float group8_sum(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  return v;
+  v += dpp<kQuadXor1>(v);
+  v += dpp<kQuadXor2>(v);
+  return v + dpp<kHalfMirror>(v);
 }
 
+// Workgroup (x, b): tensor/head th = x % 3H (0..H-1 q, H..2H-1 k, 2H..3H-1
+// v), tokens [64 (x / 3H), +64) of batch entry b; consecutive workgroups
+// take the heads of the same tokens. Lane group g (8 lanes, 8 features
+// each) handles tokens g and g + 32 of the block. Every load (features,
+// positions, then the rotary table entries) is issued before the first
+// result is computed.
 __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerWg + (threadIdx.x >> 3);
-  if (row >= p.rows) return;  // whole 8-lane groups leave together
-  const int sub = threadIdx.x & 7;
-  const int64_t h = row % p.H;
-  const int part = static_cast<int>((row / p.H) % 3);
-  const int64_t bt = row / (3 * p.H);
-  const int64_t T = p.N * p.P;
-  const int64_t t = bt % T, b = bt / T;
-
-  const u32x4 raw = *reinterpret_cast<const u32x4 *>(p.src[part] + b * p.sb[part] + t * p.st[part] +
-                                                    h * p.sh[part] + sub * 8);
-  float x[8];
+  const int32_t H = p.H, T = p.N * p.P;
+  const int32_t th = static_cast<int32_t>(blockIdx.x % (3 * H));
+  const int32_t tb = static_cast<int32_t>(blockIdx.x / (3 * H));
+  const int32_t part = th / H, h = th - part * H;
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x, sub = tid & 7;
+  const bool norm = part < 2 && p.norm[part];
+  const bool rope = part < 2 && p.pos;
+  const uint16_t *src = p.src[part] + b * p.sb[part] + h * p.sh[part] + sub * 8;
+  int32_t t[kPasses];
+  bool ok[kPasses];
+  u32x4 raw[kPasses];
+  int32_t pq[kPasses];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    x[2 * e] = bf16_to_f32(static_cast<uint16_t>(raw[e]));
-    x[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(raw[e] >> 16));
+  for (int i = 0; i < kPasses; ++i) {
+    t[i] = tb * kTokens + i * kRows + (tid >> 3);
+    ok[i] = t[i] < T;
+    const int32_t tc = ok[i] ? t[i] : T - 1;  // in-bounds stand-in for rows past the end
+    raw[i] = *reinterpret_cast<const u32x4 *>(src + static_cast<int64_t>(tc) * p.st[part]);
+    pq[i] = rope ? p.pos[b * p.pos_sb + static_cast<int64_t>(tc) * p.pos_st + (sub >> 2)] : 0;
   }
-  if (part < 2 && p.norm[part]) {
-    float s = 0.f;
+  float cs[kPasses][8], sn[kPasses][8];
+  if (rope) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s += x[e];
-    const float mean = group8_sum(s) / static_cast<float>(kHeadDim);
-    float v = 0.f;
+    for (int i = 0; i < kPasses; ++i) {
+      const int32_t q = pq[i] < 0 ? 0 : (pq[i] >= p.rope_n ? p.rope_n - 1 : pq[i]);
+      const floatx4 *c4 = reinterpret_cast<const floatx4 *>(p.rope_cos + q * 16 + (sub & 1) * 8);
+      const floatx4 *s4 = reinterpret_cast<const floatx4 *>(p.rope_sin + q * 16 + (sub & 1) * 8);
+      const floatx4 c0 = c4[0], c1 = c4[1], s0 = s4[0], s1 = s4[1];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v += (x[e] - mean) * (x[e] - mean);
-    const float var = group8_sum(v) / static_cast<float>(kHeadDim);
-    const float rstd = 1.0f / sqrtf(var + p.eps[part]);
-    const float *w = p.norm_w[part], *bb = p.norm_b[part];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float y = (x[e] - mean) * rstd;
-      if (w) y = y * w[sub * 8 + e];
-      if (bb) y = y + bb[sub * 8 + e];
-      x[e] = y;
+      for (int e = 0; e < 4; ++e) {
+        cs[i][e] = c0[e]; cs[i][e + 4] = c1[e];
+        sn[i][e] = s0[e]; sn[i][e + 4] = s1[e];
+      }
     }
   }
-  if (part < 2 && p.pos) {
-    // features [0, 32) rotate with the row position, [32, 64) with the
-    // column position; inside a half, feature j < 16 pairs with j + 16
-    const int32_t *pp = p.pos + b * p.pos_sb + t * p.pos_st;
-    int64_t pq = pp[sub >> 2];
-    pq = pq < 0 ? 0 : (pq >= p.rope_n ? p.rope_n - 1 : pq);
-    const bool first = (sub & 2) == 0;
-    float partner[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) partner[e] = __shfl_xor(x[e], 2);
-    const float *cs = p.rope_cos + pq * 16 + (sub & 1) * 8;
-    const float *sn = p.rope_sin + pq * 16 + (sub & 1) * 8;
+  float w[8], bb[8];
+  if (norm) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float rot = first ? -partner[e] : partner[e];
-      x[e] = x[e] * cs[e] + rot * sn[e];
+      w[e] = p.norm_w[part] ? p.norm_w[part][sub * 8 + e] : 1.f;
+      bb[e] = p.norm_b[part] ? p.norm_b[part][sub * 8 + e] : 0.f;
     }
   }
-  u32x4 out;
+  const int32_t np = p.N * (p.P - p.S), ns = p.N * p.S;
+  const int64_t bh = b * H + h;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(x[2 * e], x[2 * e + 1]);
-
-  const int64_t n = t / p.P, tf = t % p.P;
-  const int64_t np = p.N * (p.P - p.S), ns = p.N * p.S;
-  const bool patch = tf >= p.S;
-  const int64_t ip = n * (p.P - p.S) + (tf - p.S), is = n * p.S + tf;
-  uint16_t *dst;
-  if (part == 0)
-    dst = patch ? p.q_patch + ((b * p.H + h) * np + ip) * kHeadDim : p.q_special + ((b * p.H + h) * ns + is) * kHeadDim;
-  else
-    dst = (part == 1 ? p.k_out : p.v_out) + ((b * p.H + h) * T + (patch ? ip : np + is)) * kHeadDim;
-  *reinterpret_cast<u32x4 *>(dst + sub * 8) = out;
+  for (int i = 0; i < kPasses; ++i) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = bf16_to_f32(static_cast<uint16_t>(raw[i][e]));
+      x[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(raw[i][e] >> 16));
+    }
+    if (norm) {
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += x[e];
+      const float mean = group8_sum(s) / static_cast<float>(kHeadDim);
+      float v = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v += (x[e] - mean) * (x[e] - mean);
+      const float var = group8_sum(v) / static_cast<float>(kHeadDim);
+      const float rstd = 1.0f / sqrtf(var + p.eps[part]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = ((x[e] - mean) * rstd) * w[e] + bb[e];
+    }
+    if (rope) {
+      // features [0, 32) rotate with the row position, [32, 64) with the
+      // column position; inside a half, feature j < 16 pairs with j + 16
+      const bool first = (sub & 2) == 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float partner = dpp<kQuadXor2>(x[e]);
+        const float rot = first ? -partner : partner;
+        x[e] = x[e] * cs[i][e] + rot * sn[i][e];
+      }
+    }
+    if (!ok[i]) continue;
+    u32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(x[2 * e], x[2 * e + 1]);
+    const int32_t n = t[i] / p.P, tf = t[i] - n * p.P;
+    const bool patch = tf >= p.S;
+    const int32_t ip = n * (p.P - p.S) + (tf - p.S), is = n * p.S + tf;
+    uint16_t *dst;
+    if (part == 0)
+      dst = patch ? p.q_patch + (bh * np + ip) * kHeadDim : p.q_special + (bh * ns + is) * kHeadDim;
+    else
+      dst = (part == 1 ? p.k_out : p.v_out) + (bh * T + (patch ? ip : np + is)) * kHeadDim;
+    *reinterpret_cast<u32x4 *>(dst + sub * 8) = out;
+  }
 }
 
 struct RestoreParams {
   const uint16_t *xp, *xs;      // [B,H,Np,64] and [B,H,Ns,64], element (b,h,i,d) at x + b*sb + h*sh + i*st + d
   int64_t p_sb, p_sh, p_st, s_sb, s_sh, s_st;
-  int64_t B, H, N, P, S;
+  int32_t H, N, P, S;
   uint16_t *out;                // [B, T, H*64] contiguous
-  int64_t rows;                 // B * T * H
 };
 
+// Workgroup (x, b): head x % H, tokens [64 (x / H), +64) of batch entry b;
+// consecutive workgroups fill the heads of the same output tokens.
 __global__ __launch_bounds__(kThreads) void restore_tokens_kernel(const RestoreParams p) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerWg + (threadIdx.x >> 3);
-  if (row >= p.rows) return;
-  const int sub = threadIdx.x & 7;
-  const int64_t h = row % p.H, bt = row / p.H;
-  const int64_t T = p.N * p.P;
-  const int64_t t = bt % T, b = bt / T;
-  const int64_t n = t / p.P, tf = t % p.P;
-  const uint16_t *src = tf >= p.S
-      ? p.xp + b * p.p_sb + h * p.p_sh + (n * (p.P - p.S) + tf - p.S) * p.p_st
-      : p.xs + b * p.s_sb + h * p.s_sh + (n * p.S + tf) * p.s_st;
-  *reinterpret_cast<u32x4 *>(p.out + (bt * p.H + h) * kHeadDim + sub * 8) =
-      *reinterpret_cast<const u32x4 *>(src + sub * 8);
+  const int32_t H = p.H, T = p.N * p.P;
+  const int32_t h = static_cast<int32_t>(blockIdx.x % H);
+  const int32_t tb = static_cast<int32_t>(blockIdx.x / H);
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x, sub = tid & 7;
+  u32x4 v[kPasses];
+#pragma unroll
+  for (int i = 0; i < kPasses; ++i) {
+    const int32_t t = tb * kTokens + i * kRows + (tid >> 3);
+    if (t < T) {
+      const int32_t n = t / p.P, tf = t - n * p.P;
+      const uint16_t *src = tf >= p.S
+          ? p.xp + b * p.p_sb + h * p.p_sh + static_cast<int64_t>(n * (p.P - p.S) + tf - p.S) * p.p_st
+          : p.xs + b * p.s_sb + h * p.s_sh + static_cast<int64_t>(n * p.S + tf) * p.s_st;
+      v[i] = *reinterpret_cast<const u32x4 *>(src + sub * 8);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPasses; ++i) {
+    const int32_t t = tb * kTokens + i * kRows + (tid >> 3);
+    if (t < T) *reinterpret_cast<u32x4 *>(p.out + ((b * T + t) * H + h) * kHeadDim + sub * 8) = v[i];
+  }
 }
 
 int check_src(const char *name, const void *ptr, int64_t sb, int64_t st, int64_t sh) {
@@ -170,6 +225,8 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   VASC_SUPPORTED(d == kHeadDim, "head_dim %lld not built (built: 64)", (long long)d);
   VASC_REQUIRE(B > 0 && H > 0 && N > 0 && P > 0 && S >= 0 && S <= P, "invalid sizes B=%lld H=%lld N=%lld P=%lld S=%lld",
                (long long)B, (long long)H, (long long)N, (long long)P, (long long)S);
+  VASC_REQUIRE(B < 65536 && H < 4096 && N * P < (int64_t(1) << 31) / 64, "too many tokens or heads");
+  VASC_REQUIRE(cdiv(N * P, kTokens) * 3 * H < (int64_t(1) << 31), "grid too large");
   int rc;
   if ((rc = check_src("q", q, q_sb, q_st, q_sh))) return rc;
   if ((rc = check_src("k", k, k_sb, k_st, k_sh))) return rc;
@@ -184,6 +241,8 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   VASC_REQUIRE(k_norm == 0 || k_eps >= 0.f, "k_eps must be non-negative");
   if (pos) {
     VASC_REQUIRE(rope_cos && rope_sin && rope_n > 0, "rotary tables are required with positions");
+    VASC_REQUIRE(((reinterpret_cast<uintptr_t>(rope_cos) | reinterpret_cast<uintptr_t>(rope_sin)) & 15) == 0,
+                 "rotary tables must be 16-byte aligned");
     VASC_REQUIRE(pos_sb >= 0 && pos_st >= 2, "position strides must be pos_sb >= 0, pos_st >= 2");
   }
   PackParams p;
@@ -191,17 +250,16 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   p.sb[0] = q_sb; p.st[0] = q_st; p.sh[0] = q_sh;
   p.sb[1] = k_sb; p.st[1] = k_st; p.sh[1] = k_sh;
   p.sb[2] = v_sb; p.st[2] = v_st; p.sh[2] = v_sh;
-  p.B = B; p.H = H; p.N = N; p.P = P; p.S = S;
+  p.H = static_cast<int32_t>(H); p.N = static_cast<int32_t>(N); p.P = static_cast<int32_t>(P);
+  p.S = static_cast<int32_t>(S);
   p.norm_w[0] = q_norm_w; p.norm_b[0] = q_norm_b; p.eps[0] = q_eps; p.norm[0] = q_norm;
   p.norm_w[1] = k_norm_w; p.norm_b[1] = k_norm_b; p.eps[1] = k_eps; p.norm[1] = k_norm;
   p.pos = pos; p.pos_sb = pos_sb; p.pos_st = pos_st;
-  p.rope_cos = rope_cos; p.rope_sin = rope_sin; p.rope_n = rope_n;
+  p.rope_cos = rope_cos; p.rope_sin = rope_sin;
+  p.rope_n = static_cast<int32_t>(rope_n < (int64_t(1) << 30) ? rope_n : (int64_t(1) << 30));
   p.q_patch = q_patch; p.q_special = q_special; p.k_out = k_out; p.v_out = v_out;
-  p.rows = B * N * P * 3 * H;
-  const int64_t grid = cdiv(p.rows, kRowsPerWg);
-  VASC_REQUIRE(grid < (int64_t(1) << 31), "too many tokens");
-  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
-                     reinterpret_cast<hipStream_t>(stream), p);
+  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(cdiv(N * P, kTokens) * 3 * H), static_cast<unsigned>(B)),
+                     dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
   return check_launch("vasc_pack_qkv");
 }
 
@@ -212,6 +270,8 @@ extern "C" int vasc_restore_tokens(const uint16_t *x_patch, int64_t p_sb, int64_
   using namespace vasc;
   VASC_SUPPORTED(d == kHeadDim, "head_dim %lld not built (built: 64)", (long long)d);
   VASC_REQUIRE(B > 0 && H > 0 && N > 0 && P > 0 && S >= 0 && S <= P, "invalid sizes");
+  VASC_REQUIRE(B < 65536 && H < 4096 && N * P < (int64_t(1) << 31) / 64, "too many tokens or heads");
+  VASC_REQUIRE(cdiv(N * P, kTokens) * 3 * H < (int64_t(1) << 31), "grid too large");
   VASC_REQUIRE(out && (reinterpret_cast<uintptr_t>(out) & 15) == 0, "out must be a 16-byte aligned buffer");
   int rc;
   if (P > S && (rc = check_src("x_patch", x_patch, p_sb, p_st, p_sh))) return rc;
@@ -219,12 +279,10 @@ extern "C" int vasc_restore_tokens(const uint16_t *x_patch, int64_t p_sb, int64_
   RestoreParams p;
   p.xp = x_patch; p.p_sb = p_sb; p.p_sh = p_sh; p.p_st = p_st;
   p.xs = x_special; p.s_sb = s_sb; p.s_sh = s_sh; p.s_st = s_st;
-  p.B = B; p.H = H; p.N = N; p.P = P; p.S = S;
+  p.H = static_cast<int32_t>(H); p.N = static_cast<int32_t>(N); p.P = static_cast<int32_t>(P);
+  p.S = static_cast<int32_t>(S);
   p.out = out;
-  p.rows = B * N * P * H;
-  const int64_t grid = cdiv(p.rows, kRowsPerWg);
-  VASC_REQUIRE(grid < (int64_t(1) << 31), "too many tokens");
-  hipLaunchKernelGGL(restore_tokens_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
-                     reinterpret_cast<hipStream_t>(stream), p);
+  hipLaunchKernelGGL(restore_tokens_kernel, dim3(static_cast<unsigned>(cdiv(N * P, kTokens) * H), static_cast<unsigned>(B)),
+                     dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
   return check_launch("vasc_restore_tokens");
 }
