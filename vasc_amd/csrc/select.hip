@@ -578,8 +578,10 @@ __device__ __forceinline__ int sample_margin(int S, int c, int K) {
 // step follows every element of lower lanes and its own j' < j; ties at T
 // are kept in index order up to need when split. The kept indices go to
 // stage[0 ..) in LDS (other lanes write their trash slot stage[64 EPT +
-// lane]) and, for VASC, into the pair counts (trash counters pair_cnt[P +
-// lane]). kMask: writes the 0/1 mask (every element of the row) instead.
+// lane]) and, for VASC, into the pair counts: two 16-bit counts per word
+// (pair p in half p % 2 of word p / 2; a workgroup's rows give each pair at
+// most 2 * rows_per_workgroup), trash counters in the 64 words after them.
+// kMask: writes the 0/1 mask (every element of the row) instead.
 // Returns the number kept.
 template <bool kVasc, bool kMask, int EPT>
 __device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane, uint32_t T, int need, bool split,
@@ -627,7 +629,9 @@ __device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         stage[sel[j] ? pos : 64 * EPT + lane] = static_cast<uint32_t>(kk + j);
-        if (kVasc) atomicAdd(&pair_cnt[sel[j] ? (kk + j) >> 1 : P + lane], 1u);
+        // pair p counts in half p % 2 of word p / 2; the trash words follow
+        if (kVasc) atomicAdd(&pair_cnt[sel[j] ? (kk + j) >> 2 : ((P + 1) >> 1) + lane],
+                             sel[j] ? 1u << (((kk + j) & 2) << 3) : 1u);
         pos += sel[j] ? 1 : 0;
         run_sel += __popcll(bsel[j]);
       }
@@ -661,7 +665,7 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
   const int K = static_cast<int>(p.K);
   int gate = 0;
   if (kVasc) {
-    for (int64_t i = tid; i < p.P + 64; i += 256) pair_cnt[i] = 0;  // P pairs + 64 trash counters
+    for (int64_t i = tid; i < (p.P + 1) / 2 + 64; i += 256) pair_cnt[i] = 0;  // packed pairs + 64 trash counters
     __syncthreads();
     gate = service_gate(p);
   }
@@ -754,6 +758,9 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
           kj = order_key(gate ? A + pad : A);
           if (p.protected_mask) kj = ok && p.protected_mask[row * p.K + k] ? top : kj;
           kj = p.force_last && is_last ? top : kj;
+          // execution priority (non-negative, or FLT_MAX when protected):
+          // the key with the sign bit cleared is its float bits
+          if (p.priority_out && ok) p.priority_out[row * p.K + k] = __uint_as_float(kj & 0x7fffffffu);
         } else {
           // the raw bits with the sign flipped: the order key of any
           // non-negative, non-NaN score (others are redone below)
@@ -902,23 +909,13 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
     if (p.mask_out)
       compact_row<kVasc, true, EPT>(key, lane, T, need, split, none, tsel, nullptr, 0, nullptr,
                                     p.mask_out + row * p.K);
-    if (kVasc && p.priority_out) {
-#pragma unroll
-      for (int i = 0; i < EPT / 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int k = 256 * i + 4 * lane + j;
-          if (k < K) p.priority_out[row * p.K + k] = __uint_as_float(key[4 * i + j] & 0x7fffffffu);
-        }
-      }
-    }
     for (int i = lane; i < p.sink && run_sel + i < p.width; i += 64) irow[run_sel + i] = static_cast<int32_t>(p.K + i);
     if (lane == 0) p.count_out[row] = run_sel + p.sink;
   }
   if (kVasc) {
     __syncthreads();
     for (int64_t i = tid; i < p.P; i += 256) {
-      const uint32_t v = pair_cnt[i];
+      const uint32_t v = (pair_cnt[i >> 1] >> ((i & 1) << 4)) & 0xffffu;
       if (v) atomicAdd(&p.counts[bh * p.P + i], static_cast<int32_t>(v));
     }
   }
@@ -980,7 +977,8 @@ int launch_select_cfg(const SelectParams &p, hipStream_t s) {
   // keep the global count atomics down.
   const int64_t rows = p.BH * p.Q;
   const int rpw = static_cast<int>(rows >= 4 * 8192 ? 4 : (rows >= 2 * 8192 ? 2 : 1));
-  const size_t lds = (static_cast<size_t>(kWaves) * wave_lds_words<EPT>() + (kVasc ? static_cast<size_t>(p.P) + 64 : 0)) * 4;
+  const size_t lds =
+      (static_cast<size_t>(kWaves) * wave_lds_words<EPT>() + (kVasc ? static_cast<size_t>(p.P + 1) / 2 + 64 : 0)) * 4;
   const void *kern = reinterpret_cast<const void *>(select_kernel<kVasc, EPT>);
   int rc;
   if ((rc = reserve_lds(kern, lds))) return rc;
