@@ -153,6 +153,9 @@ def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=
 @pytest.mark.parametrize("K,Q,force_last,peak,levels", [
     (130, 65, True, 1.0, None), (7, 3, False, 3.0, None), (518, 40, False, 2.0, 4), (31, 9, True, 5.0, 2),
     (4096, 9, True, 2.0, None), (3000, 7, False, 1.0, 8),
+    # every register-row width of the arrival pass (16 to 64 elements per lane) and, past
+    # 4096 key blocks, the LDS-row arrival kernel
+    (1501, 5, True, 2.0, None), (2047, 6, False, 3.0, None), (2304, 3, True, 1.0, None), (5001, 4, True, 2.0, None),
 ])
 def test_vasc_chain_bit_exact(K, Q, force_last, peak, levels):
     topk = max(int(K * 0.25), 1)

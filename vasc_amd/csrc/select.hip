@@ -18,10 +18,11 @@
 // Selection keeps the c largest priorities, ties to the lower block index.
 //
 // Launches (VASC mode), each reading the fp32 score matrix once:
-//   arrival  one workgroup per (32-row chunk, head), 4-16 waves, one wave per row: the
-//            row arrives in LDS by DMA; risk total, conservative arrival and
-//            pair reductions read it there in the canonical lane order, and
-//            the chunk's float64 column partials of the pair arrival are
+//   arrival  one workgroup per (32-row chunk, head), one wave per row: the
+//            row arrives in registers (K <= 4096; lane j holds elements
+//            j + 64 m, the canonical lane order) or in LDS by DMA (larger
+//            K); risk total, conservative arrival and pair reductions, and
+//            the chunk's float64 column partials of the pair arrival
 //            accumulated in row order;
 //   head     per head: ledger settlement, arrival mean, pair capacity,
 //            admitted debt, the head's partials of the global gate;
@@ -241,6 +242,142 @@ __global__ __launch_bounds__(1024) void arrival_kernel(const SelectParams p, int
   for (int i = 0; i < kMaxPairsPerThread; ++i) {
     const int64_t pp = tid + static_cast<int64_t>(blockDim.x) * i;
     if (pp < p.P) out[pp] = part[i];
+  }
+}
+
+// Arrival for rows of at most 64 * EPT key blocks, with the row in
+// registers instead of an LDS buffer: lane j loads elements j + 64 m (m <
+// EPT) with coalesced dword loads, which is exactly the lane order of the
+// canonical wave sums; several waves per SIMD hide the load latency. The
+// innovation of the head sits in LDS; the pair
+// partner A[k + 1] of an even lane comes from its right neighbour by DPP.
+// Rows, arithmetic and the float64 column partials (thread t: pairs t,
+// t + 256, ... of the four rows of a group, in row order) are those of
+// arrival_kernel.
+template <int EPT>
+__global__ __launch_bounds__(256) void arrival_reg_kernel(const SelectParams p) {
+  extern __shared__ __attribute__((aligned(16))) float alds[];
+  constexpr int kRowWaves = 4;
+  constexpr int kPairs = (64 * EPT / 2 + 255) / 256;  // column partials per thread
+  const int P = static_cast<int>(p.P), K = static_cast<int>(p.K);
+  float *iota_s = alds;   // [P]
+  float *apair = alds + P;  // [kRowWaves][P]
+  const int64_t chunk = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t q0 = chunk * kChunk;
+  const int nrows = static_cast<int>(p.Q - q0 < kChunk ? p.Q - q0 : kChunk);
+  for (int i = tid; i < P; i += 256) iota_s[i] = p.innovation[bh * P + i];
+  double part[kPairs];
+#pragma unroll
+  for (int i = 0; i < kPairs; ++i) part[i] = 0.0;
+  __syncthreads();
+
+  // The row is read through buffer resources rebased every 16 elements, so
+  // every offset is the lane's 4 * lane plus an immediate below 4096, and
+  // elements past the row end read as 0 (raw buffer range check against
+  // num_records) without touching memory.
+  auto load = [&](float (&x)[EPT], int r, int ln) {
+    const float *srow = p.score + (bh * p.Q + q0 + r) * p.K;
+#pragma unroll
+    for (int g = 0; g < (EPT + 15) / 16; ++g) {
+      const int left = K - 1024 * g;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float *>(srow + (left > 0 ? 1024 * g : 0)), 0, left > 0 ? 4 * left : 0, 0x00020000);
+#pragma unroll
+      for (int m = 16 * g; m < EPT && m < 16 * g + 16; ++m)
+        x[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 4 * ln + 256 * (m - 16 * g), 0, 0));
+    }
+  };
+  auto process = [&](float (&x)[EPT], int r, int ln) {
+    const int64_t row = bh * p.Q + q0 + r;
+    int cap;
+    if (p.row_cap) {
+      cap = p.row_cap[row];
+    } else {
+      cap = p.topk < 1 ? 1 : p.topk;
+      cap = cap > K ? K : cap;
+      if (p.force_last && cap < K) {
+        const int mlast = (K - 1) >> 6, llast = (K - 1) & 63;
+        uint32_t last = 0;
+#pragma unroll
+        for (int m = 0; m < EPT; ++m)
+          if (m == mlast) last = order_key(__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(x[m]), llast)));
+        int beat = 0;
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) {
+          const int k = ln + 64 * m;
+          const uint32_t kk = order_key(x[m]);
+          const bool in = k < K;
+          beat += in && ((kk > last) || (kk == last && k < K - 1));
+        }
+        cap += wave_sum_int(beat) >= cap ? 1 : 0;
+      }
+    }
+    // Elements past the row end become risk +0.0 and pair value +0.0: adding
+    // +0.0 to a sum that started at +0.0 leaves it bit-identical, so every
+    // element runs the same branch-free code.
+    double acc = 0.0;
+#pragma unroll
+    for (int m = 0; m < EPT; ++m) {
+      const int k = ln + 64 * m;
+      const bool in = k < K;
+      const float risk = clean_score(x[m]) * iota_s[(in ? k : K - 1) >> 1];
+      x[m] = in ? risk : 0.f;
+      acc = acc + static_cast<double>(x[m]);
+    }
+    const float total = static_cast<float>(wave_butterfly(acc));
+    const float scale = static_cast<float>(cap) / floor_tiny(total);
+    const bool live = total > 0.f;
+    const bool even = (ln & 1) == 0;
+    double racc = 0.0;
+    float *ap_row = apair + w * P;
+#pragma unroll
+    for (int m = 0; m < EPT; ++m) {
+      const int k = ln + 64 * m;
+      const bool in = k < K;
+      const float A = live && in ? clamp01(x[m] * scale) : 0.f;
+      // right neighbour inside the 16-lane row (even lanes never sit at a row end)
+      const float An = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(A), 0x101, 0xf, 0xf, false));
+      const float ap = (k + 1 < K) ? (A + An) / 2.0f : (A + 0.0f) / 1.0f;
+      if (in && even) ap_row[k >> 1] = ap;
+      racc = racc + static_cast<double>(in && even ? ap : 0.f);
+    }
+    const float rowpair = static_cast<float>(wave_butterfly(racc));
+    if (ln == 0) {
+      p.total[row] = total;
+      p.rowpair[row] = rowpair;
+      p.cap[row] = cap;
+    }
+  };
+  auto accumulate = [&](int rows_here) {
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+      const int pp = tid + 256 * i;
+      if (pp < P)
+        for (int rr = 0; rr < rows_here; ++rr) part[i] = part[i] + static_cast<double>(apair[rr * P + pp]);
+    }
+  };
+
+  float x[EPT];
+  for (int r0 = 0; r0 < nrows; r0 += kRowWaves) {
+    if (r0 + w < nrows) {
+      // an opaque copy of the lane index keeps the per-element offsets and
+      // row-end masks inside the loop instead of hoisted into registers
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      load(x, r0 + w, ln);
+      process(x, r0 + w, ln);
+    }
+    __syncthreads();
+    accumulate(nrows - r0 < kRowWaves ? nrows - r0 : kRowWaves);
+    __syncthreads();
+  }
+  double *out = p.part + (bh * p.nchunks + chunk) * p.P;
+#pragma unroll
+  for (int i = 0; i < kPairs; ++i) {
+    const int pp = tid + 256 * i;
+    if (pp < P) out[pp] = part[i];
   }
 }
 
@@ -1008,18 +1145,43 @@ int launch_select(const SelectParams &p, bool vasc, hipStream_t s) {
   return vasc ? launch_select_mode<true>(p, s) : launch_select_mode<false>(p, s);
 }
 
+template <int EPT>
+int launch_arrival_reg_cfg(const SelectParams &p, hipStream_t s) {
+  const size_t lds = static_cast<size_t>(5 * p.P) * 4;  // innovation + four rows of pair arrivals
+  const void *kern = reinterpret_cast<const void *>(arrival_reg_kernel<EPT>);
+  int rc;
+  if ((rc = reserve_lds(kern, lds))) return rc;
+  hipLaunchKernelGGL(arrival_reg_kernel<EPT>, dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)),
+                     dim3(256), lds, s, p);
+  return VASC_OK;
+}
+int launch_arrival_reg(const SelectParams &p, hipStream_t s) {
+  const int64_t K = p.K;
+  if (K <= 512) return launch_arrival_reg_cfg<8>(p, s);
+  if (K <= 1024) return launch_arrival_reg_cfg<16>(p, s);
+  if (K <= 1536) return launch_arrival_reg_cfg<24>(p, s);
+  if (K <= 2048) return launch_arrival_reg_cfg<32>(p, s);
+  if (K <= 2304) return launch_arrival_reg_cfg<36>(p, s);
+  if (K <= 3072) return launch_arrival_reg_cfg<48>(p, s);
+  return launch_arrival_reg_cfg<64>(p, s);
+}
+
 int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
   const int64_t bufn = row_buf_elems(p.K);
   int rc;
   if (vasc) {
-    // As many waves per chunk (16, 8 or 4) as keep the row buffers within
-    // 64 KB; the column partials then need P <= 16 * (64 * waves).
-    int aw = 16;
-    while (aw > 4 && static_cast<size_t>(aw) * bufn * 4 > 64 * 1024) aw >>= 1;
-    const size_t lds = static_cast<size_t>(aw) * bufn * 4;
-    if ((rc = reserve_lds(reinterpret_cast<const void *>(arrival_kernel), lds))) return rc;
-    hipLaunchKernelGGL(arrival_kernel, dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)),
-                       dim3(64 * aw), lds, s, p, static_cast<int>(bufn));
+    if (p.K <= 64 * 64) {
+      if ((rc = launch_arrival_reg(p, s))) return rc;
+    } else {
+      // As many waves per chunk (16, 8 or 4) as keep the row buffers within
+      // 64 KB; the column partials then need P <= 16 * (64 * waves).
+      int aw = 16;
+      while (aw > 4 && static_cast<size_t>(aw) * bufn * 4 > 64 * 1024) aw >>= 1;
+      const size_t lds = static_cast<size_t>(aw) * bufn * 4;
+      if ((rc = reserve_lds(reinterpret_cast<const void *>(arrival_kernel), lds))) return rc;
+      hipLaunchKernelGGL(arrival_kernel, dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)),
+                         dim3(64 * aw), lds, s, p, static_cast<int>(bufn));
+    }
     if ((rc = check_launch("vasc_select_blocks/arrival"))) return rc;
     hipLaunchKernelGGL(head_kernel, dim3(static_cast<unsigned>(cdiv(p.P, 256)), static_cast<unsigned>(p.BH)),
                        dim3(256), 0, s, p);
