@@ -252,13 +252,13 @@ __global__ __launch_bounds__(1024) void arrival_kernel(const SelectParams p, int
 // innovation of the head sits in LDS; the pair
 // partner A[k + 1] of an even lane comes from its right neighbour by DPP.
 // Rows, arithmetic and the float64 column partials (thread t: pairs t,
-// t + 256, ... of the four rows of a group, in row order) are those of
-// arrival_kernel.
-template <int EPT>
-__global__ __launch_bounds__(256) void arrival_reg_kernel(const SelectParams p) {
+// t + 64 kRowWaves, ... of the kRowWaves rows of a group, in row order) are
+// those of arrival_kernel.
+template <int EPT, int kRowWaves>
+__global__ __launch_bounds__(64 * kRowWaves) void arrival_reg_kernel(const SelectParams p) {
   extern __shared__ __attribute__((aligned(16))) float alds[];
-  constexpr int kRowWaves = 4;
-  constexpr int kPairs = (64 * EPT / 2 + 255) / 256;  // column partials per thread
+  constexpr int kThreads = 64 * kRowWaves;
+  constexpr int kPairs = (64 * EPT / 2 + kThreads - 1) / kThreads;  // column partials per thread
   const int P = static_cast<int>(p.P), K = static_cast<int>(p.K);
   float *iota_s = alds;   // [P]
   float *apair = alds + P;  // [kRowWaves][P]
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256) void arrival_reg_kernel(const SelectParams p) 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t q0 = chunk * kChunk;
   const int nrows = static_cast<int>(p.Q - q0 < kChunk ? p.Q - q0 : kChunk);
-  for (int i = tid; i < P; i += 256) iota_s[i] = p.innovation[bh * P + i];
+  for (int i = tid; i < P; i += kThreads) iota_s[i] = p.innovation[bh * P + i];
   double part[kPairs];
 #pragma unroll
   for (int i = 0; i < kPairs; ++i) part[i] = 0.0;
@@ -298,11 +298,7 @@ __global__ __launch_bounds__(256) void arrival_reg_kernel(const SelectParams p) 
       cap = p.topk < 1 ? 1 : p.topk;
       cap = cap > K ? K : cap;
       if (p.force_last && cap < K) {
-        const int mlast = (K - 1) >> 6, llast = (K - 1) & 63;
-        uint32_t last = 0;
-#pragma unroll
-        for (int m = 0; m < EPT; ++m)
-          if (m == mlast) last = order_key(__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(x[m]), llast)));
+        const uint32_t last = order_key(p.score[row * p.K + K - 1]);  // wave-uniform load
         int beat = 0;
 #pragma unroll
         for (int m = 0; m < EPT; ++m) {
@@ -340,8 +336,13 @@ __global__ __launch_bounds__(256) void arrival_reg_kernel(const SelectParams p) 
       // right neighbour inside the 16-lane row (even lanes never sit at a row end)
       const float An = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(A), 0x101, 0xf, 0xf, false));
       const float ap = (k + 1 < K) ? (A + An) / 2.0f : (A + 0.0f) / 1.0f;
+      // the summand is fixed before the store's branch, so the row sum stays
+      // one in-order chain instead of per-element doubles summed afterwards
+      float add = in && even ? ap : 0.f;
+      asm volatile("" : "+v"(add));
+      racc = racc + static_cast<double>(add);
+      asm volatile("" : "+v"(racc));
       if (in && even) ap_row[k >> 1] = ap;
-      racc = racc + static_cast<double>(in && even ? ap : 0.f);
     }
     const float rowpair = static_cast<float>(wave_butterfly(racc));
     if (ln == 0) {
@@ -351,9 +352,11 @@ __global__ __launch_bounds__(256) void arrival_reg_kernel(const SelectParams p) 
     }
   };
   auto accumulate = [&](int rows_here) {
+    int t = tid;
+    asm volatile("" : "+v"(t));  // addresses made here, not held across the row loop
 #pragma unroll
     for (int i = 0; i < kPairs; ++i) {
-      const int pp = tid + 256 * i;
+      const int pp = t + kThreads * i;
       if (pp < P)
         for (int rr = 0; rr < rows_here; ++rr) part[i] = part[i] + static_cast<double>(apair[rr * P + pp]);
     }
@@ -376,7 +379,7 @@ __global__ __launch_bounds__(256) void arrival_reg_kernel(const SelectParams p) 
   double *out = p.part + (bh * p.nchunks + chunk) * p.P;
 #pragma unroll
   for (int i = 0; i < kPairs; ++i) {
-    const int pp = tid + 256 * i;
+    const int pp = tid + kThreads * i;
     if (pp < P) out[pp] = part[i];
   }
 }
@@ -1145,14 +1148,19 @@ int launch_select(const SelectParams &p, bool vasc, hipStream_t s) {
   return vasc ? launch_select_mode<true>(p, s) : launch_select_mode<false>(p, s);
 }
 
+// Rows of up to 36 elements per lane fit in 128 VGPRs: eight row waves per
+// chunk then give four waves per SIMD on grids of a few hundred chunks.
+// Wider rows keep four row waves (two waves per SIMD, register bound).
 template <int EPT>
 int launch_arrival_reg_cfg(const SelectParams &p, hipStream_t s) {
-  const size_t lds = static_cast<size_t>(5 * p.P) * 4;  // innovation + four rows of pair arrivals
-  const void *kern = reinterpret_cast<const void *>(arrival_reg_kernel<EPT>);
+  constexpr int kRowWaves = EPT <= 36 ? 8 : 4;
+  const size_t lds = static_cast<size_t>((1 + kRowWaves) * p.P) * 4;  // innovation + pair arrivals per row wave
+  const void *kern = reinterpret_cast<const void *>(arrival_reg_kernel<EPT, kRowWaves>);
   int rc;
   if ((rc = reserve_lds(kern, lds))) return rc;
-  hipLaunchKernelGGL(arrival_reg_kernel<EPT>, dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)),
-                     dim3(256), lds, s, p);
+  hipLaunchKernelGGL((arrival_reg_kernel<EPT, kRowWaves>),
+                     dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)), dim3(64 * kRowWaves), lds,
+                     s, p);
   return VASC_OK;
 }
 int launch_arrival_reg(const SelectParams &p, hipStream_t s) {
