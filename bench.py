@@ -216,6 +216,18 @@ def run_c5(dev) -> int:
             listed = int(sel["count"].sum().item())
             t = median_ms(lambda: ops.select_blocks(prob, **kw), 5)
             lines.append((name, t, H * qb * kb * 4 + listed * 4 + H * qb * 4, f"cap {topk} of {kb}"))
+        # cdf-threshold counts (sort + sequential running sum per row); the
+        # threshold array is built once so only the kernel is timed
+        count = torch.empty(1, H, qb, device=dev, dtype=torch.int32)
+        for thr in (0.5, 0.9):
+            T_h = torch.full((H,), thr, dtype=torch.float32).add_(1e-5).to(dev)
+            def cdf(T_h=T_h):
+                _lib.call("vasc_cdf_counts", prob.data_ptr(), 1, H, qb, kb, T_h.data_ptr(), 0, 0, count.data_ptr(),
+                          None, ops._stream())
+            cdf()
+            mean_n = float(count.float().mean().item())
+            t = median_ms(cdf, 5)
+            lines.append(("cdf_counts", t, H * qb * kb * 4 + H * qb * 4, f"threshold {thr}, mean count {mean_n:.1f}"))
         t = median_ms(lambda: ops.pack_v(v), 5)
         lines.append(("pack_v", t, hbm["pack_v"], None))
         for name, t, nbytes, note in lines:

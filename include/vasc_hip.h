@@ -117,12 +117,16 @@ size_t vasc_select_workspace_size(int64_t B, int64_t H, int64_t q_blocks,
  * score       [B,H,Q,K] float32 contiguous pooled probabilities.
  * innovation  [B,H,ceil(K/2)] float32 (VASC only).
  * topk        base budget int(K*(1-s)); the fill rule raises 0 to 1.
- * row_cap     optional [B,H,Q] int32 per-row QK budget (VASC); NULL derives
- *             it from topk and force_last as block_sparse_attn_cuda does.
+ * row_cap     optional [B,H,Q] int32 per-row budget; NULL derives it from
+ *             topk (and, in VASC, force_last) as block_sparse_attn_cuda does.
+ *             TOPK: the per-row count (cdf threshold, vasc_cdf_counts), the
+ *             forced tail added on top, each at most max_capacity (0 = K).
+ *             VASC: the row's QK capacity (base count including the tail).
  * protected_mask optional [B,H,Q,K] uint8 (VASC): priority FLT_MAX.
  * force_last  mixed tail block K-1: kept in TOPK, protected in VASC and
  *             counted in the derived capacity (sparse_wrapper.py:7599-7662).
- * max_capacity M (VASC): at most M blocks per row (the capacity hint).
+ * max_capacity M (VASC): at most M blocks per row (the capacity hint);
+ *             TOPK with row_cap: the largest row_cap entry (0 = K).
  * sink_blocks trailing always-on blocks K..K+sink-1 appended to each list.
  * debt_in, pending_arrival, prev_service [B,H,P] float32, each may be NULL
  *             (NULL pending = no previous layer to settle).
@@ -155,6 +159,27 @@ int vasc_select_blocks(const float *score, const float *innovation,
 int vasc_settle_terminal(const float *debt_in, const float *pending_arrival,
                          const float *service, int64_t n, float *debt_out,
                          void *stream);
+
+/*
+ * Per-row counts of get_block_mask's cdf-threshold branch
+ * (sparse_wrapper.py:1238-1254; fill rule ZIP:spas_sage_attn/utils.py:289).
+ * Replaces the torch.sort + torch.cumsum + torch.searchsorted sequence.
+ *
+ * score       [B,H,Q,K] float32 contiguous pooled probabilities.
+ * thresholds  [H] float32 device array T_h = f32(thr_h + eps).
+ * count_out   [B,H,Q] int32: length of the prefix of the descending row
+ *             whose sequential float32 running sum stays <= T_h, raised to
+ *             min_count (the ratio budget when a ratio is also given), and
+ *             at least 1.
+ * base_out    optional [B,H,Q] int32: count plus the forced mixed tail
+ *             (force_last and block K-1 not among the first `count`), the
+ *             row capacity the VASC selector takes.
+ * Built variant: K <= 8192.
+ */
+int vasc_cdf_counts(const float *score, int64_t B, int64_t H, int64_t Q,
+                    int64_t K, const float *thresholds, int32_t min_count,
+                    int32_t force_last, int32_t *count_out, int32_t *base_out,
+                    void *stream);
 
 /* Elements (bf16) of the packed V buffer for these sizes. */
 int64_t vasc_packed_v_elems(int64_t B, int64_t H, int64_t nk, int64_t d);

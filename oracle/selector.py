@@ -7,6 +7,10 @@ Follows ``src/sparse_vggt/utils/sparse_wrapper.py`` (``SW``) of the reference:
 * ``topk_block_mask``      ``get_block_mask`` ratio/top-k branch
                            (``SW:1199-1268``) with the fill kernel's min-1
                            rule (``spas_sage_attn/utils.py:283-292``).
+* ``cdf_counts``,          its cdf-threshold branch (``SW:1238-1254``):
+  ``cdf_block_mask``       sequential float32 running sum over the
+                           descending row, prefix count against
+                           ``thr + eps``.
 * ``innovation``           pair innovation of pooled values (``SW:3733-3740``).
 * ``cosa_select``          ``get_cosa_value_risk_pair_debt_mask``
                            (``SW:3632-4098``) in the release ``vasc``
@@ -31,7 +35,9 @@ finite priority, memory activates, terminal settlement idempotent) and closed
 forms: layer 0 priority equals the conservative arrival, uniform innovation
 without saturation reduces to Top-K on the score, zero innovation selects the
 first ``cap`` indices, zero debt disables the gate, brute-force Top-K on tiny
-rows.
+rows. The cdf count is pinned against torch's own sort / cumsum /
+searchsorted (the reference's primitives) on dyadic scores, where every
+prefix sum is exact, and against a brute-force loop and closed forms.
 """
 from __future__ import annotations
 
@@ -108,6 +114,61 @@ def topk_block_mask(score: np.ndarray, sink_blocks: int, topk: int | None = None
     if sink_blocks > 0:
         sink = np.ones(sel.shape[:-1] + (sink_blocks,), dtype=bool)
         sel = np.concatenate([sel, sink], axis=-1)
+    return sel
+
+
+def head_thresholds(cdf_threshold, H: int) -> np.ndarray:
+    """Per-head float32 thresholds: ``hyperparameter_check``
+    (``spas_sage_attn/utils.py:38-50``) broadcasts a number to every head and
+    takes a 1-D sequence of ``H`` values as given."""
+    t = np.asarray(cdf_threshold, dtype=np.float32)
+    if t.ndim == 0:
+        return np.full(H, t, dtype=np.float32)
+    if t.ndim != 1 or t.size != H:
+        raise AssertionError(f"Hyperparameter tensor must have {H} elements")
+    return t
+
+
+def cdf_counts(score: np.ndarray, cdf_threshold, topk: int | None = None, eps: float = 1e-5) -> np.ndarray:
+    """``num_to_select`` of ``get_block_mask``'s cdf branch (``SW:1238-1254``)
+    after the fill kernel's min-1 rule (``spas_sage_attn/utils.py:289``).
+
+    Each row is ordered by descending ``order_key`` (NaN first, as torch's
+    descending sort), its running float32 sum is taken strictly in that order,
+    and the count is the length of the prefix whose running sum stays
+    ``<= T_h`` with ``T_h = f32(f32(thr_h) + f32(eps))``. For non-negative
+    scores (softmax output) the running sum never decreases and the count
+    equals ``torch.searchsorted(cdf, T, right=True)``. ``topk`` (the ratio
+    budget when both are given) is a lower bound; a count of 0 becomes 1.
+    The reference's cumsum is torch's CUDA scan; the canonical order here is
+    sequential (the two round alike except where a prefix sum lies within an
+    ulp of the threshold).
+    """
+    s = np.asarray(score, dtype=np.float32)
+    B, H, Q, K = s.shape
+    T = (head_thresholds(cdf_threshold, H) + np.float32(eps)).astype(np.float32)
+    key = order_key(s)
+    order = np.argsort(key, axis=-1, kind="stable")[..., ::-1]
+    canon = np.where(s == 0, np.float32(0.0), np.where(np.isnan(s), np.float32(np.nan), s))
+    vals = np.take_along_axis(canon, order, axis=-1)
+    cdf = np.cumsum(vals, axis=-1, dtype=np.float32)  # ufunc accumulate: strictly sequential
+    over = ~(cdf <= T.reshape(1, H, 1, 1))
+    n = np.where(over.any(-1), np.argmax(over, axis=-1), K).astype(np.int64)
+    if topk is not None:
+        n = np.maximum(n, int(topk))
+    return np.where(n == 0, 1, n).astype(np.int32)
+
+
+def cdf_block_mask(score: np.ndarray, sink_blocks: int, cdf_threshold, sparse_ratio: float | None = None,
+                   eps: float = 1e-5) -> np.ndarray:
+    """``get_block_mask`` with ``cdf_threshold`` (alone or with a ratio):
+    the ``cdf_counts`` largest pooled scores of each row (ties to the lower
+    index) plus ``sink`` trailing always-on columns."""
+    K = score.shape[-1]
+    topk = None if sparse_ratio is None else ratio_to_topk(K, sparse_ratio)
+    sel = select_top(score, cdf_counts(score, cdf_threshold, topk, eps))
+    if sink_blocks > 0:
+        sel = np.concatenate([sel, np.ones(sel.shape[:-1] + (sink_blocks,), dtype=bool)], axis=-1)
     return sel
 
 
@@ -343,21 +404,27 @@ def finalize(state: dict) -> dict:
 # --------------------------------------------------------------------------
 # block_sparse_attn_cuda selection wiring (SW:6998-7041, 7559-7770)
 # --------------------------------------------------------------------------
-def layer_selection(score, *, mode: str, sparse_ratio: float, patch_tokens: int,
+def layer_selection(score, *, mode: str, sparse_ratio: float | None, patch_tokens: int,
                     total_tokens: int, official_mask: bool, state: dict | None = None,
-                    layer_idx: int = 0, pooled_value=None, iota=None, block_k: int = 64):
+                    layer_idx: int = 0, pooled_value=None, iota=None, block_k: int = 64,
+                    cdf_threshold=None):
     """Final block map ``[B,H,Q,Kb+sink]`` for ``mode`` in {topk, vasc}.
 
-    Mirrors the default branch of ``block_sparse_attn_cuda``: Top-K base map
-    with sink columns, the mixed-tail rule (forced + protected unless the
-    official mask is requested) and, in vasc mode, the CoSA selector with
-    ``hint = int(Kb*(1-s)) + [protected]``.
+    Mirrors the default branch of ``block_sparse_attn_cuda``: base map from
+    ``get_block_mask`` (ratio, cdf, or both) with sink columns, the mixed-tail
+    rule (forced + protected unless the official mask is requested) and, in
+    vasc mode, the CoSA selector with ``hint = int(Kb*(1-s)) + [protected]``
+    for the ratio alone and no hint (``M = max cap``) when a cdf threshold is
+    given (``SW:7744-7750``).
     """
     Kb = score.shape[-1]
     total_blocks = math.ceil(total_tokens / block_k)
     sink = total_blocks - Kb
     mixed = patch_tokens < total_tokens and patch_tokens % block_k != 0
-    final = topk_block_mask(score, sink, sparse_ratio=sparse_ratio)
+    if cdf_threshold is None:
+        final = topk_block_mask(score, sink, sparse_ratio=sparse_ratio)
+    else:
+        final = cdf_block_mask(score, sink, cdf_threshold, sparse_ratio=sparse_ratio)
     force_last = mixed and not official_mask
     if force_last:
         final[..., Kb - 1] = True
@@ -370,7 +437,7 @@ def layer_selection(score, *, mode: str, sparse_ratio: float, patch_tokens: int,
         protected = np.zeros(score.shape, bool)
         protected[..., Kb - 1] = True
     cap = final[..., :Kb].sum(-1)
-    hint = ratio_to_topk(Kb, sparse_ratio) + int(protected is not None)
+    hint = None if cdf_threshold is not None else ratio_to_topk(Kb, sparse_ratio) + int(protected is not None)
     sel, info = cosa_select(score, pooled_value, cap, layer_idx=layer_idx, state=state,
                             protected=protected, max_capacity_hint=hint, iota=iota)
     final = np.concatenate([sel, final[..., Kb:]], axis=-1)

@@ -155,6 +155,44 @@ def test_block_sparse_attn_c1_end_to_end(release_env, model):
                               np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("model,mode", [("pi3", "topk"), ("pi3", "vasc"), ("vggt", "vasc")])
+def test_block_sparse_attn_c1_cdf_threshold(release_env, model, mode):
+    """Config 1 through block_sparse_attn_cuda with a cdf threshold (and a
+    ratio lower bound for Pi3 top-k): the sparsity equals the oracle's block
+    map, attention is within tolerance on the oracle's lists and the VASC
+    ledger matches bit for bit."""
+    from vasc_amd import ops
+    from vasc_amd.attention import predict_attention
+    from vasc_amd.sparse_wrapper import block_sparse_attn_cuda
+    release_env(model, mode)
+    N, P, S, H, D = 8, 1041, 5, 16, 64
+    Np, Tk = N * (P - S), N * P
+    ratio = 0.9 if mode == "topk" else None
+    g = torch.Generator().manual_seed(6)
+    st_gpu, st_ref = {}, {}
+    for layer in range(2):
+        q = torch.randn(1, H, Np, D, generator=g).to(torch.bfloat16)
+        k = torch.randn(1, H, Tk, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, H, Tk, D, generator=g).to(torch.bfloat16)
+        qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+        score = predict_attention(qc, kc[:, :, :Np])
+        out, sparsity = block_sparse_attn_cuda(qc, kc, vc, score, sparse_ratio=ratio, cdf_threshold=0.5,
+                                               return_sparsity=True, layer_idx=layer, routing_state=st_gpu,
+                                               num_patch_tokens=Np)
+        _, _, _, iota = ops.pool_qkv(v=vc[:, :, :Np])
+        final, _ = OS.layer_selection(score.cpu().numpy(), mode=mode, sparse_ratio=ratio, cdf_threshold=0.5,
+                                      patch_tokens=Np, total_tokens=Tk, official_mask=(model == "vggt"),
+                                      state=st_ref, layer_idx=layer, iota=iota.cpu().numpy())
+        idx, cnt = OS.index_lists(final)
+        assert abs(float(sparsity) - (1 - final.mean())) < 1e-6
+        ref = OA.block_sparse_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), idx, cnt)
+        err = np.abs(out.float().cpu().numpy() - ref)
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
+        if mode == "vasc":
+            assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_debt"]),
+                                  np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
+
+
 def test_global_layer_forward_dense_limit():
     """adaptive_sparse_attention_forward at sparsity 0 equals dense attention of
     the same module (all key blocks kept)."""

@@ -177,3 +177,95 @@ def test_vasc_c2_shape_chain():
 def test_vasc_c3_shape_two_layers():
     """Config 3 shape: H=16, 1036 x 2072 blocks at s=0.875 structural (224 blocks)."""
     _run_chain(2072, 1036, 16, 2, topk=224, force_last=False, sink=10, peak=2.0, seed=3)
+
+
+# ---------------------------------------------------------------- cdf threshold
+@pytest.mark.parametrize("K,Q,H,levels", [(7, 3, 2, None), (130, 65, 2, 4), (518, 20, 4, None), (2072, 6, 2, None),
+                                          (5000, 3, 2, 2), (8192, 2, 1, None)])
+def test_cdf_counts_bit_exact(K, Q, H, levels):
+    """Per-row cdf counts and the capacity with the forced tail vs the oracle
+    (scalar and per-head thresholds, the ratio lower bound, thresholds that
+    keep a single block and the whole row)."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(K)
+    score = _scores(rng, (1, H, Q, K), peak=3.0, levels=levels)
+    s = torch.from_numpy(score).cuda()
+    for thr in (0.0, 0.3, 0.9, 1.0, [0.5 + 0.1 * h for h in range(H)]):
+        for min_count, fl in ((0, False), (max(K // 8, 1), True), (0, True)):
+            n = OS.cdf_counts(score, thr, min_count)
+            cnt, base = ops.cdf_counts(s, thr, min_count=min_count, force_last=fl, want_base=True)
+            assert np.array_equal(cnt.cpu().numpy(), n), (thr, min_count)
+            last_in = OS.select_top(score, n)[..., K - 1]
+            assert np.array_equal(base.cpu().numpy(), n + (fl & ~last_in & (n < K))), (thr, min_count, fl)
+
+
+def test_cdf_counts_on_prefix_boundaries():
+    """Dyadic scores: thresholds on, just under and within eps of exact prefix sums."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(21)
+    K = 300
+    score = (rng.integers(0, 65, size=(1, 2, 8, K)) / 1024).astype(np.float32)
+    p = float(np.cumsum(-np.sort(-score[0, 0, 0]))[K // 3])
+    for thr in (p, p - 2e-5, p - 5e-6):
+        cnt, _ = ops.cdf_counts(torch.from_numpy(score).cuda(), thr)
+        assert np.array_equal(cnt.cpu().numpy(), OS.cdf_counts(score, thr)), thr
+
+
+@pytest.mark.parametrize("K,sink", [(130, 1), (518, 3), (2072, 0)])
+def test_topk_row_counts_with_forced_tail_bit_exact(K, sink):
+    """Top-K selection with per-row counts (cdf) plus the forced mixed tail and
+    sink columns, including rows that keep every block."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(K + 1)
+    score = _scores(rng, (1, 2, 9, K), peak=2.0, levels=3)
+    n = OS.cdf_counts(score, [0.5, 1.0])
+    sel = OS.select_top(score, n)
+    sel[..., K - 1] = True
+    s = torch.from_numpy(score).cuda()
+    cnt, _ = ops.cdf_counts(s, [0.5, 1.0])
+    out = ops.select_blocks(s, mode=TOPK, topk=0, row_cap=cnt, force_last=True, sink_blocks=sink, want_mask=True)
+    assert np.array_equal(out["mask"].cpu().numpy().astype(bool), sel)
+    _assert_lists(out, sel, sink)
+
+
+def test_get_block_mask_cdf_bit_exact():
+    from vasc_amd.sparse_wrapper import get_block_mask
+    rng = np.random.default_rng(22)
+    score = _scores(rng, (1, 4, 65, 130), peak=3.0)
+    s = torch.from_numpy(score).cuda()
+    for kw in (dict(cdf_threshold=0.7), dict(cdf_threshold=0.4, sparse_ratio=0.9), dict(cdf_threshold=0.0)):
+        got = get_block_mask(s, 1, **kw).cpu().numpy()
+        ref = OS.cdf_block_mask(score, 1, kw["cdf_threshold"], sparse_ratio=kw.get("sparse_ratio"))
+        assert np.array_equal(got, ref), kw
+
+
+def test_vasc_chain_cdf_capacity_bit_exact():
+    """VASC selector with per-row capacities from the cdf threshold (no
+    capacity hint: M is the largest row capacity) and the protected mixed
+    tail, four chained layers."""
+    from vasc_amd import ops
+    K, Q, H = 130, 65, 2
+    rng = np.random.default_rng(23)
+    st = {}
+    debt = pending = service = None
+    for layer in range(4):
+        score = _scores(rng, (1, H, Q, K), peak=2.5)
+        iota = OS.innovation(rng.standard_normal((1, H, K, 64)).astype(np.float32))
+        base_mask = OS.select_top(score, OS.cdf_counts(score, 0.6))
+        base_mask[..., K - 1] = True
+        cap = base_mask.sum(-1)
+        prot = np.zeros((1, H, Q, K), bool)
+        prot[..., K - 1] = True
+        sel, info = OS.cosa_select(score, None, cap, layer_idx=layer, state=st, protected=prot, iota=iota)
+        s = torch.from_numpy(score).cuda()
+        _, base = ops.cdf_counts(s, 0.6, force_last=True, want_base=True)
+        assert np.array_equal(base.cpu().numpy(), cap)
+        out = ops.select_blocks(s, mode=VASC, topk=0, innovation=torch.from_numpy(iota).cuda(), row_cap=base,
+                                force_last=True, max_capacity=int(base.max()), debt=debt, pending_arrival=pending,
+                                prev_service=service, want_priority=True, want_mask=True)
+        assert np.array_equal(_bits(out["priority"].cpu()), _bits(info["priority"])), f"layer {layer}: priority"
+        assert np.array_equal(out["mask"].cpu().numpy().astype(bool), sel), f"layer {layer}: support"
+        _assert_lists(out, sel, 0)
+        for key in ("debt", "arrival", "service"):
+            assert np.array_equal(_bits(out[key].cpu()), _bits(info[key])), f"layer {layer}: {key}"
+        debt, pending, service = out["debt"], out["arrival"], out["service"]

@@ -71,7 +71,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES), "ctypes table out of sync with include/vasc_hip.h"
-    assert lib.vasc_abi_version() == 2
+    assert lib.vasc_abi_version() == 3
 
 
 def test_host_only_queries_and_argument_errors():
@@ -115,3 +115,11 @@ def test_host_only_queries_and_argument_errors():
     rc = lib.vasc_global_attn_fwd(None, 0, 0, 8, None, 0, 0, 8, None, 0, 0, 8, None, None, 0, 0, 8,
                                   None, 0, 0, 8, 1, 1, 128, 32, 64, 64, None, 1, None, f(0.125), None)
     assert rc == 1 and b"q_special" in lib.vasc_last_error()
+    # cdf counts: pointers, the built key-block range and the ratio floor (never dereferenced here)
+    fake = ctypes.c_void_p(256)
+    rc = lib.vasc_cdf_counts(None, 1, 16, 259, 518, fake, 0, 0, fake, None, None)
+    assert rc == 1 and b"required" in lib.vasc_last_error()
+    rc = lib.vasc_cdf_counts(fake, 1, 16, 259, 9000, fake, 0, 0, fake, None, None)
+    assert rc == 2 and b"8192" in lib.vasc_last_error()
+    rc = lib.vasc_cdf_counts(fake, 1, 16, 259, 518, fake, 519, 0, fake, None, None)
+    assert rc == 1 and b"min_count" in lib.vasc_last_error()

@@ -147,3 +147,85 @@ def test_layer_selection_mixed_tail(official):
     assert np.array_equal(final_v[..., :130].sum(-1), final[..., :130].sum(-1))
     if not official:
         assert final_v[..., 129].all()
+
+
+# ---------------------------------------------------------------- cdf threshold
+def _torch_cdf_counts(score, thr, topk=None, eps=1e-5):
+    """get_block_mask's cdf steps (SW:1238-1254) and the fill rule
+    (utils.py:289) with torch's own sort / cumsum / searchsorted."""
+    import torch
+    s = torch.from_numpy(score)
+    B, H, Q, K = s.shape
+    cdf = torch.cumsum(torch.sort(s, dim=-1, descending=True).values, dim=-1)
+    t = torch.as_tensor(thr, dtype=torch.float32)
+    t = torch.full((H,), float(t)) if t.ndim == 0 else t
+    t = (t.view(1, H, 1, 1) + eps).expand(B, -1, Q, 1).contiguous()
+    n = torch.searchsorted(cdf, t, right=True).squeeze(-1)
+    if topk is not None:
+        n = torch.clamp(n, min=topk)
+    return torch.where(n == 0, torch.ones_like(n), n).numpy()
+
+
+@pytest.mark.parametrize("K", [1, 7, 64, 130, 518])
+def test_cdf_counts_match_torch_on_dyadic_scores(K):
+    """Scores k/1024: every prefix sum is exact in float32 (and float64), so
+    torch's scan and the sequential sum agree bit for bit. Thresholds sit
+    exactly on prefix sums, just below them and in between."""
+    rng = np.random.default_rng(K)
+    s = (rng.integers(0, 65, size=(1, 3, 5, K)) / 1024).astype(np.float32)
+    cdf = np.cumsum(-np.sort(-s, axis=-1), axis=-1)
+    p = float(cdf[0, 0, 0, K // 2])
+    picks = [0.0, p, p - 2e-5, p - 5e-6, 0.37, float(cdf.max()) + 1.0]  # p - 5e-6 is kept only through eps
+    for thr in picks:
+        for topk in (None, 0, max(K // 4, 1)):
+            got = OS.cdf_counts(s, thr, topk)
+            assert np.array_equal(got, _torch_cdf_counts(s, thr, topk)), (thr, topk)
+    per_head = [0.1, 0.25, 0.5]
+    assert np.array_equal(OS.cdf_counts(s, per_head), _torch_cdf_counts(s, np.array(per_head, np.float32)))
+
+
+def test_cdf_counts_sequential_float32_brute_force():
+    """Non-dyadic softmax rows: the running sum is the strictly sequential
+    float32 one (a loop over the descending row)."""
+    rng = np.random.default_rng(11)
+    s = _softmax(rng.standard_normal((1, 2, 6, 37)) * 2)
+    for thr in (0.3, 0.6, 0.9, 0.99):
+        got = OS.cdf_counts(s, thr)
+        T = np.float32(np.float32(thr) + np.float32(1e-5))
+        for h, q in itertools.product(range(2), range(6)):
+            row = np.sort(s[0, h, q])[::-1]
+            acc, n = np.float32(0.0), 0
+            for v in row:
+                acc = np.float32(acc + v)
+                if not acc <= T:
+                    break
+                n += 1
+            assert got[0, h, q] == max(n, 1)
+
+
+def test_cdf_counts_closed_forms():
+    K = 256
+    u = np.full((1, 1, 2, K), 1.0 / K, np.float32)  # cdf[i] = (i+1)/K exactly
+    assert (OS.cdf_counts(u, 0.5) == K // 2).all()
+    assert (OS.cdf_counts(u, 1.0) == K).all()          # the full sum 1.0 <= 1 + eps
+    assert (OS.cdf_counts(u, 0.0) == 1).all()          # nothing fits: fill rule keeps one block
+    assert (OS.cdf_counts(u, 0.0, topk=5) == 5).all()  # the ratio budget is a lower bound
+    # without the eps, a threshold equal to a prefix sum keeps it anyway (right=True)
+    assert (OS.cdf_counts(u, 0.25, eps=0.0) == K // 4).all()
+    # uniform rows select the first n blocks (ties to the lower index)
+    m = OS.cdf_block_mask(u, 2, 0.125)
+    assert m[..., : K // 8].all() and not m[..., K // 8 : K].any() and m[..., K:].all()
+
+
+def test_layer_selection_cdf_vasc_capacity_is_row_count():
+    s = _softmax(np.random.default_rng(12).standard_normal((1, 2, 65, 130)) * 3)
+    final, _ = OS.layer_selection(s, mode="topk", sparse_ratio=None, cdf_threshold=0.6, patch_tokens=8288,
+                                  total_tokens=8328, official_mask=False)
+    n = OS.cdf_counts(s, 0.6)
+    last_in = OS.select_top(s, n)[..., 129]
+    assert np.array_equal(final[..., :130].sum(-1), n + (~last_in))  # forced mixed tail
+    final_v, _ = OS.layer_selection(s, mode="vasc", sparse_ratio=None, cdf_threshold=0.6, patch_tokens=8288,
+                                    total_tokens=8328, official_mask=False, state={}, layer_idx=0,
+                                    pooled_value=np.random.default_rng(13).standard_normal((1, 2, 130, 64)))
+    assert np.array_equal(final_v[..., :130].sum(-1), final[..., :130].sum(-1))
+    assert final_v[..., 129].all()

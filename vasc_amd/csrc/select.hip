@@ -92,6 +92,87 @@ struct SelectParams {
   int64_t nchunks;
 };
 
+// ------------------------------------------------------------- cdf counts
+// get_block_mask's cdf branch (sparse_wrapper.py:1238-1254) and the fill
+// rule (ZIP:spas_sage_attn/utils.py:289). One workgroup per row: the row's
+// order keys are sorted descending in LDS (bitonic; padding keys 0 sort
+// last), then one lane walks the sorted values with a strictly sequential
+// float32 running sum and counts the prefix that stays <= T_h. The count is
+// raised to min_count (the ratio budget when both are given) and a count of
+// 0 becomes 1. base_out (optional) adds the forced mixed tail: one more block
+// when at least `count` other blocks beat the last one (greater key, or an
+// equal key at a lower index), i.e. when the last block is not among the
+// first `count` of the row.
+__device__ __forceinline__ float key_value(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+__global__ __launch_bounds__(256) void cdf_count_kernel(const float *score, int64_t H, int64_t Q, int K, int n2,
+                                                        const float *thr, int32_t min_count, int32_t force_last,
+                                                        int32_t *count_out, int32_t *base_out) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t ckeys[];  // [n2], read 16 bytes at a time
+  __shared__ int sbeat;
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float *srow = score + row * K;
+  const uint32_t last = order_key(srow[K - 1]);
+  if (tid == 0) sbeat = 0;
+  __syncthreads();
+  int beat = 0;
+  for (int k = tid; k < n2; k += 256) {
+    const uint32_t kk = k < K ? order_key(srow[k]) : 0u;
+    ckeys[k] = kk;
+    beat += k < K - 1 && kk >= last;
+  }
+  if (force_last && base_out) atomicAdd(&sbeat, beat);
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (int t = tid; t < (n2 >> 1); t += 256) {
+        const int i = ((t & ~(stride - 1)) << 1) | (t & (stride - 1)), j = i + stride;  // stride: a power of two
+        const uint32_t a = ckeys[i], b = ckeys[j];
+        const bool desc = (i & size) == 0;
+        if (desc ? a < b : a > b) {
+          ckeys[i] = b;
+          ckeys[j] = a;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const float T = thr[(row / Q) % H];
+    // 64 sorted keys per batch (16 LDS reads in flight; n2 is a multiple of
+    // 64); the running sum is the only serial chain.
+    const uint4 *k4 = reinterpret_cast<const uint4 *>(ckeys);
+    float acc = 0.f;
+    int n = 0;
+    bool go = true;
+    for (int b = 0; go && 64 * b < K; ++b) {
+      uint4 q[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) q[j] = k4[16 * b + j];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t kq[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 64 * b + 4 * j + e;
+          const float next = acc + key_value(kq[e]);
+          const bool ok = go && i < K && next <= T;
+          n = ok ? i + 1 : n;
+          acc = ok ? next : acc;
+          go = ok;
+        }
+      }
+    }
+    n = n > min_count ? n : min_count;
+    n = n == 0 ? 1 : (n > K ? K : n);
+    count_out[row] = n;
+    if (base_out) base_out[row] = n + ((force_last && n < K && sbeat >= n) ? 1 : 0);
+  }
+}
+
 // ------------------------------------------------------------------ settle
 // Settled debt of one ledger entry (sparse_wrapper.py:3793-3832).
 __device__ __forceinline__ float settle_one(const SelectParams &p, int64_t i, float *refl, float *sig) {
@@ -859,7 +940,12 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
       total = p.total[row];
       scale = static_cast<float>(cap) / floor_tiny(total);
     } else {
-      c = p.topk < 1 ? 1 : p.topk;
+      // per-row counts (cdf threshold) or the uniform budget; the index
+      // width was sized for max_capacity (plus the forced tail)
+      c = p.row_cap ? p.row_cap[row] : p.topk;
+      c = c < 1 ? 1 : c;
+      const int lim = p.max_capacity >= K ? K : p.max_capacity - p.force_last;
+      if (p.row_cap) c = c < lim ? c : lim;
       c = c > K ? K : c;
       last = order_key(srow[K - 1]);
     }
@@ -1236,7 +1322,8 @@ extern "C" int vasc_select_blocks(const float *score, const float *innovation, i
     VASC_REQUIRE(!prev_service || pending_arrival, "prev_service without pending_arrival");
     maxc = max_capacity < K ? max_capacity : K;
   } else {
-    int64_t t = topk < 1 ? 1 : topk;
+    // row_cap: per-row counts, each at most max_capacity (K when 0)
+    int64_t t = row_cap ? (max_capacity > 0 ? max_capacity : K) : (topk < 1 ? 1 : topk);
     maxc = t + (force_last ? 1 : 0);
     maxc = maxc < K ? maxc : K;
   }
@@ -1294,4 +1381,21 @@ extern "C" int vasc_settle_terminal(const float *debt_in, const float *pending_a
   hipLaunchKernelGGL(settle_terminal_kernel, dim3(cdiv(n, 256)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
                      debt_in, pending_arrival, service, n, debt_out);
   return check_launch("vasc_settle_terminal");
+}
+
+extern "C" int vasc_cdf_counts(const float *score, int64_t B, int64_t H, int64_t Q, int64_t K,
+                               const float *thresholds, int32_t min_count, int32_t force_last, int32_t *count_out,
+                               int32_t *base_out, void *stream) {
+  using namespace vasc;
+  VASC_REQUIRE(score && thresholds && count_out, "score, thresholds and count_out are required");
+  VASC_REQUIRE(B > 0 && H > 0 && Q > 0 && K > 0, "sizes must be positive");
+  VASC_SUPPORTED(K <= 8192, "K=%lld key blocks not built (built: <= 8192)", (long long)K);
+  VASC_REQUIRE(min_count >= 0 && min_count <= K, "min_count %d outside [0, K]", min_count);
+  VASC_REQUIRE(B * H * Q < (int64_t(1) << 31), "too many rows");
+  int n2 = 64;
+  while (n2 < K) n2 <<= 1;
+  hipLaunchKernelGGL(cdf_count_kernel, dim3(static_cast<unsigned>(B * H * Q)), dim3(256),
+                     static_cast<size_t>(n2) * 4, reinterpret_cast<hipStream_t>(stream), score, H, Q,
+                     static_cast<int>(K), n2, thresholds, min_count, force_last, count_out, base_out);
+  return check_launch("vasc_cdf_counts");
 }

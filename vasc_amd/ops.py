@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -120,9 +121,12 @@ def select_blocks(score: torch.Tensor, *, mode: int, topk: int, innovation=None,
     vasc = mode == _lib.MODE_VASC
     dev = s.device
     if vasc:
-        maxc = min(int(max_capacity), K)
+        maxc = mc_arg = min(int(max_capacity), K)
+    elif row_cap is not None:  # per-row counts, each at most max_capacity (0 = K), plus the forced tail
+        mc_arg = int(max_capacity)
+        maxc = min((mc_arg if mc_arg > 0 else K) + int(bool(force_last)), K)
     else:
-        maxc = min(max(int(topk), 1) + int(bool(force_last)), K)
+        maxc = mc_arg = min(max(int(topk), 1) + int(bool(force_last)), K)
     width = maxc + sink_blocks if width is None else int(width)
     out = {
         "index": torch.empty(B, H, Q, max(width, 1), device=dev, dtype=torch.int32),
@@ -151,12 +155,38 @@ def select_blocks(score: torch.Tensor, *, mode: int, topk: int, innovation=None,
             raise ValueError(f"{name} must hold B*H*P={B * H * P} values")
     ws_bytes = workspace.numel() if workspace is not None else 0
     _lib.call("vasc_select_blocks", s.data_ptr(), _ptr(inn), B, H, Q, K, int(mode), int(topk), _ptr(rc),
-              _ptr(pm), int(bool(force_last)), int(maxc), int(sink_blocks), _ptr(state[0]),
+              _ptr(pm), int(bool(force_last)), int(mc_arg), int(sink_blocks), _ptr(state[0]),
               _ptr(state[1]), _ptr(state[2]), _ptr(out.get("debt")), _ptr(out.get("arrival")),
               _ptr(out.get("service")), _ptr(out.get("gate")), _ptr(out.get("priority")),
               _ptr(out.get("mask")), out["index"].data_ptr(), width, out["count"].data_ptr(),
               _ptr(workspace), ws_bytes, _stream())
     return out
+
+
+def cdf_counts(score: torch.Tensor, cdf_threshold, *, min_count: int = 0, force_last: bool = False,
+               eps: float = 1e-5, want_base: bool = False):
+    """Per-row counts of ``get_block_mask``'s cdf-threshold branch (kernel 2).
+
+    ``cdf_threshold``: a number or ``H`` per-head values
+    (``hyperparameter_check``); the kernel compares against
+    ``f32(f32(thr) + f32(eps))``. Returns ``(count, base)`` int32 ``[B,H,Q]``
+    (``base`` adds the forced mixed tail, ``None`` unless ``want_base``).
+    """
+    _dev(score, "score")
+    s = score.float().contiguous()
+    B, H, Q, K = s.shape
+    thr = cdf_threshold.detach().float().cpu().numpy() if isinstance(cdf_threshold, torch.Tensor) else cdf_threshold
+    thr = np.asarray(thr, dtype=np.float32)
+    if thr.ndim == 0:
+        thr = np.full(H, thr, dtype=np.float32)
+    if thr.ndim != 1 or thr.size != H:
+        raise ValueError(f"cdf_threshold must be a number or hold {H} values")
+    T = torch.from_numpy((thr + np.float32(eps)).astype(np.float32)).to(s.device)
+    count = torch.empty(B, H, Q, device=s.device, dtype=torch.int32)
+    base = torch.empty_like(count) if want_base else None
+    _lib.call("vasc_cdf_counts", s.data_ptr(), B, H, Q, K, T.data_ptr(), int(min_count), int(bool(force_last)),
+              count.data_ptr(), _ptr(base), _stream())
+    return count, base
 
 
 def settle_terminal(debt, pending_arrival, service) -> torch.Tensor:

@@ -77,29 +77,39 @@ def _require_gpu(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be a GPU tensor (this operator has no CPU path)")
 
 
-def _budget(key_blocks: int, topk, sparse_ratio, cdf_threshold) -> int:
+def _budget(key_blocks: int, topk, sparse_ratio, cdf_threshold) -> int | None:
+    """The uniform budget ``int(Kb*(1-s))`` or ``topk`` (SW:1224-1235);
+    ``None`` for the cdf threshold alone."""
     check_sparse_mode_three_type(topk, sparse_ratio, cdf_threshold)
-    if cdf_threshold is not None:
-        raise NotImplementedError("cdf_threshold selection is not built; use sparse_ratio or topk")
     if sparse_ratio is not None:
         assert 0 <= sparse_ratio <= 1
         topk = int(key_blocks * (1 - sparse_ratio))
-    assert 0 <= topk <= key_blocks
-    return int(topk)
+    if topk is not None:
+        assert 0 <= topk <= key_blocks
+    if cdf_threshold is not None:
+        thr = cdf_threshold.detach().cpu() if isinstance(cdf_threshold, torch.Tensor) else cdf_threshold
+        assert bool((torch.as_tensor(thr) >= 0).all() and (torch.as_tensor(thr) <= 1).all())
+    return None if topk is None else int(topk)
 
 
 def get_block_mask(pooled_score: torch.Tensor, sink_blocks: int, topk: int | None = None,
                    sparse_ratio: float | None = None, cdf_threshold: float | None = None,
                    eps: float = 1e-5) -> torch.Tensor:
-    """Top-k block map with ``sink_blocks`` trailing always-on columns.
+    """Block map with ``sink_blocks`` trailing always-on columns (SW:1199-1268).
 
-    Returns bool ``[B,H,Q,K+sink]`` with ``max(topk,1)`` patch blocks per row.
+    Returns bool ``[B,H,Q,K+sink]`` with ``max(topk,1)`` patch blocks per row,
+    or with a cdf threshold the per-row count of ``ops.cdf_counts`` (at least
+    the ratio budget when both are given).
     """
     _require_gpu(pooled_score, "pooled_score")
     B, H, Q, K = pooled_score.shape
     assert 0 <= sink_blocks <= K
     t = _budget(K, topk, sparse_ratio, cdf_threshold)
-    out = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=t, want_mask=True)
+    if cdf_threshold is not None:
+        count, _ = ops.cdf_counts(pooled_score, cdf_threshold, min_count=t or 0, eps=eps)
+        out = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=0, row_cap=count, want_mask=True)
+    else:
+        out = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=t, want_mask=True)
     mask = out["mask"].bool()
     if sink_blocks > 0:
         mask = torch.cat([mask, mask.new_ones(B, H, Q, sink_blocks)], dim=-1)
@@ -306,6 +316,10 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
     t = _budget(orig_kblk, topk, sparse_ratio, cdf_threshold)
     mixed = num_patch_tokens is not None and num_patch_tokens < Tk and num_patch_tokens % KBLK != 0
     force_last = mixed and not cfg.official_mask
+    count = base = None
+    if cdf_threshold is not None:
+        count, base = ops.cdf_counts(pooled_score, cdf_threshold, min_count=t or 0, force_last=force_last,
+                                     want_base=cfg.mode == "vasc")
     if cfg.mode == "vasc":
         if num_patch_tokens is None:
             raise ValueError("CoSA pair debt requires patch metadata")
@@ -314,17 +328,24 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
         B, H = pooled_score.shape[:2]
         P = (orig_kblk + 1) // 2
         _, _, _, innovation = ops.pool_qkv(v=value[..., :num_patch_tokens, :])
-        hint = (t + int(force_last)) if (sparse_ratio is not None and topk is None) else None
-        if hint is None:
-            hint = max(t, 1) + int(force_last)
+        if base is not None:
+            # no hint with a cdf threshold: M is the largest row capacity (SW:3709-3712)
+            hint = int(base.max())
+        else:
+            hint = (t + int(force_last)) if (sparse_ratio is not None and topk is None) else None
+            if hint is None:
+                hint = max(t, 1) + int(force_last)
         debt, pending, service = _ledger_inputs(routing_state, B, H, P)
-        sel = ops.select_blocks(pooled_score, mode=_lib.MODE_VASC, topk=t, innovation=innovation,
-                                force_last=force_last, max_capacity=hint, sink_blocks=sink, debt=debt,
+        sel = ops.select_blocks(pooled_score, mode=_lib.MODE_VASC, topk=t or 0, innovation=innovation,
+                                row_cap=base, force_last=force_last, max_capacity=hint, sink_blocks=sink, debt=debt,
                                 pending_arrival=pending, prev_service=service,
                                 want_priority=not cfg.skip_routing_stats)
         _ledger_outputs(routing_state, sel, pooled_score, layer_idx, min(hint, orig_kblk))
         if routing_stats_store is not None:
             routing_stats_store.update(_stats(sel, None))
+    elif count is not None:
+        sel = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=0, row_cap=count, force_last=force_last,
+                                sink_blocks=sink)
     else:
         sel = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=t, force_last=force_last,
                                 sink_blocks=sink)
