@@ -1235,11 +1235,12 @@ int launch_select(const SelectParams &p, bool vasc, hipStream_t s) {
 }
 
 // Rows of up to 36 elements per lane fit in 128 VGPRs: eight row waves per
-// chunk then give four waves per SIMD on grids of a few hundred chunks.
+// chunk then give four waves per SIMD on grids of a few hundred chunks; rows
+// of up to 16 elements (K <= 1024, grids of ~150 chunks at C2) take sixteen.
 // Wider rows keep four row waves (two waves per SIMD, register bound).
 template <int EPT>
 int launch_arrival_reg_cfg(const SelectParams &p, hipStream_t s) {
-  constexpr int kRowWaves = EPT <= 36 ? 8 : 4;
+  constexpr int kRowWaves = EPT <= 16 ? 16 : (EPT <= 36 ? 8 : 4);
   const size_t lds = static_cast<size_t>((1 + kRowWaves) * p.P) * 4;  // innovation + pair arrivals per row wave
   const void *kern = reinterpret_cast<const void *>(arrival_reg_kernel<EPT, kRowWaves>);
   int rc;
