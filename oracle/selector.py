@@ -296,6 +296,22 @@ def qk_service(selected: np.ndarray, patch_blocks: int) -> np.ndarray:
     return (counts.astype(np.float32) / denom).astype(np.float32)
 
 
+def pv_execution_service(execution_map: np.ndarray, patch_blocks: int) -> np.ndarray:
+    """PV-execution service per pair (``_reduce_exact_pv_execution_to_pair``,
+    SW:2983-3028): executed children per pair summed over query blocks, query
+    warps and the pair, over ``query_warps * pair_size`` with ``query_warps =
+    Q * W``. ``execution_map`` binary ``[B,H,Q,W,K]``. Returns float32
+    ``[B,H,P]``."""
+    ex = np.asarray(execution_map)[..., :patch_blocks].astype(np.int64)
+    if patch_blocks % 2:
+        ex = np.concatenate([ex, np.zeros(ex.shape[:-1] + (1,), np.int64)], axis=-1)
+    P = (patch_blocks + 1) // 2
+    counts = ex.reshape(ex.shape[:-1] + (P, 2)).sum(axis=(-1, -3, -4))  # pair, warp, query block
+    query_warps = execution_map.shape[-3] * execution_map.shape[-2]
+    denom = (np.float32(query_warps) * _pair_size(patch_blocks)).astype(np.float32)
+    return (counts.astype(np.float32) / denom).astype(np.float32)
+
+
 def cosa_select(score, pooled_value, cap, *, layer_idx: int, state: dict,
                 protected=None, max_capacity_hint: int | None = None,
                 iota=None):

@@ -37,6 +37,11 @@ def release_env(request):
     os.environ.update(saved)
 
 
+def _softmax_rows(rng, shape):
+    x = rng.standard_normal(shape)
+    return (np.exp(x) / np.exp(x).sum(-1, keepdims=True)).astype(np.float32)
+
+
 def _bits(t):
     return np.ascontiguousarray(t.detach().float().cpu().numpy()).view(np.uint32)
 
@@ -93,8 +98,9 @@ def test_get_block_mask_bit_exact():
     assert np.array_equal(m, OS.topk_block_mask(s, 0, topk=0))
 
 
-def test_cosa_mask_api_chain_bit_exact():
+def test_cosa_mask_api_chain_bit_exact(release_env):
     from vasc_amd import sparse_wrapper as SW
+    release_env("pi3", "vasc")  # QK-admission service, as the reference's check_selector sets it
     rng = np.random.default_rng(3)
     st_gpu, st_ref = {}, {}
     B, H, Q, K = 1, 2, 9, 31
@@ -191,6 +197,55 @@ def test_block_sparse_attn_c1_cdf_threshold(release_env, model, mode):
         if mode == "vasc":
             assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_debt"]),
                                   np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
+
+
+def test_pv_execution_service_domain_chain(release_env):
+    """DEBT_SERVICE_DOMAIN=pv_execution (the reference's default): the
+    selector leaves the service to the attention launch, so a second selector
+    call without attention in between fails as the reference's does; through
+    block_sparse_attn_cuda the observed PV-execution service (every wave
+    executes every listed block, threshold inert) drives the same ledger bits
+    as the oracle's."""
+    from vasc_amd import ops
+    from vasc_amd import sparse_wrapper as SW
+    from vasc_amd.attention import predict_attention
+    release_env("pi3", "vasc")
+    os.environ["SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN"] = "pv_execution"
+    rng = np.random.default_rng(8)
+    s = torch.from_numpy(_softmax_rows(rng, (1, 2, 9, 31))).cuda()
+    pv = torch.from_numpy(rng.standard_normal((1, 2, 31, 64)).astype(np.float32)).cuda()
+    base = torch.ones(1, 2, 9, 31, dtype=torch.bool, device="cuda")
+    st = {}
+    SW.get_cosa_value_risk_pair_debt_mask(s, pv, base, layer_idx=0, routing_state=st, fp32_projection=True)
+    assert SW.SERVICE_KEY not in st
+    with pytest.raises(RuntimeError, match="PV service identity"):
+        SW.get_cosa_value_risk_pair_debt_mask(s, pv, base, layer_idx=1, routing_state=st, fp32_projection=True)
+
+    N, P, S, H, D = 4, 1041, 5, 16, 64
+    Np, Tk = N * (P - S), N * P
+    g = torch.Generator().manual_seed(9)
+    st_gpu, st_ref = {}, {}
+    for layer in range(3):
+        q = torch.randn(1, H, Np, D, generator=g).to(torch.bfloat16)
+        k = torch.randn(1, H, Tk, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, H, Tk, D, generator=g).to(torch.bfloat16)
+        qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+        score = predict_attention(qc, kc[:, :, :Np])
+        SW.block_sparse_attn_cuda(qc, kc, vc, score, sparse_ratio=0.75, layer_idx=layer, routing_state=st_gpu,
+                                  num_patch_tokens=Np)
+        obs = st_gpu[SW.SERVICE_KEY]
+        assert obs["identity_observed"] and obs["layer_idx"] == layer and "service_domain" not in obs
+        _, _, _, iota = ops.pool_qkv(v=vc[:, :, :Np])
+        final, _ = OS.layer_selection(score.cpu().numpy(), mode="vasc", sparse_ratio=0.75, patch_tokens=Np,
+                                      total_tokens=Tk, official_mask=False, state=st_ref, layer_idx=layer,
+                                      iota=iota.cpu().numpy())
+        Kb = score.shape[-1]
+        ex = np.broadcast_to(final[:, :, :, None, :Kb], final.shape[:3] + (4, Kb))
+        assert np.array_equal(_bits(obs["pair_service_fraction"][:, :, 0]),
+                              OS.pv_execution_service(ex, Kb).view(np.uint32))
+        assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_debt"]),
+                              np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
+    assert SW.finalize_cosa_value_risk_pair_debt(st_gpu)
 
 
 def test_global_layer_forward_dense_limit():

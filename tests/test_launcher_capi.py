@@ -44,9 +44,20 @@ def test_routing_config_resolves_release_modes():
 def test_routing_config_rejects_research_switches():
     env = launcher.method_environment("vggt", "vasc")
     for extra in ({"SPARSE_VGGT_COSA_ORDERED_LUT": "1"}, {"SPARSE_VGGT_QK_PV_THRESHOLD": "sequence_mass_bound"},
-                  {"SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN": "pv_execution"}):
+                  {"SPARSE_VGGT_QK_PV_THRESHOLD": "4.0", "SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN": "pv_execution"}):
         with pytest.raises(NotImplementedError):
             launcher.routing_config({**env, **extra})
+    with pytest.raises(ValueError):  # as the reference selector (SW:3999-4000)
+        launcher.routing_config({**env, "SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN": "pv_count"})
+
+
+def test_routing_config_service_domains():
+    env = launcher.method_environment("pi3", "vasc")
+    assert launcher.routing_config(env).service_domain == "qk_admission"
+    cfg = launcher.routing_config({**env, "SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN": "pv_execution"})
+    assert cfg.mode == "vasc" and cfg.service_domain == "pv_execution"
+    env.pop("SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN")  # the reference's default domain
+    assert launcher.routing_config(env).service_domain == "pv_execution"
 
 
 def test_allocation_settings():

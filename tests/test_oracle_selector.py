@@ -229,3 +229,27 @@ def test_layer_selection_cdf_vasc_capacity_is_row_count():
                                     pooled_value=np.random.default_rng(13).standard_normal((1, 2, 130, 64)))
     assert np.array_equal(final_v[..., :130].sum(-1), final[..., :130].sum(-1))
     assert final_v[..., 129].all()
+
+
+# ---------------------------------------------------------------- PV-execution service
+@pytest.mark.parametrize("K", [7, 130, 518])
+def test_pv_execution_service_equals_qk_admission_when_every_wave_executes(K):
+    """With the PV threshold inert every query warp of a block executes every
+    selected child: the exact PV-execution reduction and the QK-admission
+    fraction are the same float32 values (the same integers divided)."""
+    rng = np.random.default_rng(K)
+    Q, W = 9, 4
+    sel = rng.random((1, 3, Q, K)) < 0.3
+    sel[..., 0] = True
+    ex = np.broadcast_to(sel[:, :, :, None, :], (1, 3, Q, W, K)).astype(np.int32)
+    assert np.array_equal(OS.pv_execution_service(ex, K).view(np.uint32), OS.qk_service(sel, K).view(np.uint32))
+
+
+def test_pv_execution_service_counts_skipped_warps():
+    """A warp that skips a child lowers that pair's service by 1/(Q*W*pair_size)."""
+    Q, W, K = 2, 4, 5  # pairs (0,1), (2,3), (4)
+    ex = np.ones((1, 1, Q, W, K), np.int32)
+    ex[0, 0, 1, 2, 4] = 0
+    ex[0, 0, 0, 0, 1] = 0
+    got = OS.pv_execution_service(ex, K)[0, 0]
+    assert np.allclose(got, [1 - 1 / (Q * W * 2), 1.0, 1 - 1 / (Q * W)])

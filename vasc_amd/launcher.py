@@ -111,6 +111,7 @@ class RoutingConfig:
     mode: str = "vasc"          # "topk" or "vasc" (dense never reaches the op)
     official_mask: bool = False  # VGGT: no forced/protected mixed-tail block
     skip_routing_stats: bool = True
+    service_domain: str = "qk_admission"  # ledger service: "qk_admission" or "pv_execution"
 
 
 def routing_config(env=None) -> RoutingConfig:
@@ -128,10 +129,11 @@ def routing_config(env=None) -> RoutingConfig:
                                "COSA_RISK_SAFE_OBSERVER", "QK_VALUE_RISK_OBSERVER", "QK_BUNDLE_OBSERVER",
                                "COLLECT_QK_PV_SERVICE", "RADIAL_A_DENSE", "RADIAL_A_CHUNKED")
                    if _flag(env, n)]
+    domain = "qk_admission"
     if vasc:
         domain = env.get("SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN", "pv_execution").lower()
-        if domain != "qk_admission":
-            unsupported.append(f"COSA_DEBT_SERVICE_DOMAIN={domain}")
+        if domain not in ("qk_admission", "pv_execution"):
+            raise ValueError("unsupported CoSA debt service domain")
         if not _flag(env, "COSA_CONSERVATIVE_ARRIVAL_PROJECTION"):
             unsupported.append("COSA_CONSERVATIVE_ARRIVAL_PROJECTION=0")
         if not _flag(env, "COSA_CONSERVATIVE_DEBT_PROJECTION"):
@@ -145,4 +147,4 @@ def routing_config(env=None) -> RoutingConfig:
     if unsupported:
         raise NotImplementedError("switches outside the release modes: " + ", ".join(unsupported))
     return RoutingConfig(mode="vasc" if vasc else "topk", official_mask=_flag(env, "OFFICIAL_MASK"),
-                         skip_routing_stats=_flag(env, "SKIP_ROUTING_STATS"))
+                         skip_routing_stats=_flag(env, "SKIP_ROUTING_STATS"), service_domain=domain)

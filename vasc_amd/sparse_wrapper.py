@@ -24,6 +24,7 @@ unspecified).
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 
@@ -35,6 +36,7 @@ STATE_KEY = "cosa_value_risk_pair_debt"
 PENDING_KEY = "cosa_value_risk_pair_pending_arrival"
 PENDING_LAYER_KEY = "cosa_value_risk_pair_pending_layer"
 SERVICE_KEY = "qk_pv_service_observation"
+_PV_SERVICE_PENDING = "_vasc_pv_execution_service"  # service awaiting the attention launch
 
 # Research keyword arguments of block_sparse_attn_cuda (SW:6868-6971) with the
 # values the release modes pass; any other value selects a research router
@@ -143,7 +145,7 @@ def _ledger_inputs(routing_state: dict, B: int, H: int, P: int):
         if obs.get("layer_idx") != routing_state.get(PENDING_LAYER_KEY):
             raise RuntimeError("PV service does not match pending CoSA layer")
         if "pair_service_fraction" not in obs:
-            raise NotImplementedError("only the qk_admission service domain is built")
+            raise RuntimeError("PV service observation carries no pair service fraction")
         service = obs["pair_service_fraction"]
         if tuple(service.shape) != shape:
             raise RuntimeError("PV service changed the stable pair layout")
@@ -152,23 +154,64 @@ def _ledger_inputs(routing_state: dict, B: int, H: int, P: int):
     return debt, pending, service
 
 
-def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_idx: int, M: int) -> None:
+def _service_domain() -> str:
+    """``SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN`` (SW:3996-4000; default pv_execution)."""
+    domain = os.environ.get("SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN", "pv_execution").lower()
+    if domain not in ("pv_execution", "qk_admission"):
+        raise ValueError("unsupported CoSA debt service domain")
+    return domain
+
+
+def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_idx: int, M: int,
+                    domain: str = "qk_admission") -> None:
+    """State writes of the selector (SW:3990-4025). In the QK-admission domain
+    the service observation is recorded here; in the PV-execution domain the
+    attention launch records it (``_record_pv_execution``)."""
     B, H, Q, K = score.shape
     P = (K + 1) // 2
     routing_state[STATE_KEY] = out["debt"].view(B, H, 1, P)
     routing_state[PENDING_KEY] = out["arrival"].view(B, H, 1, P)
     routing_state[PENDING_LAYER_KEY] = int(layer_idx)
-    routing_state[SERVICE_KEY] = {
-        "layer_idx": int(layer_idx),
-        "identity_observed": True,
-        "service_domain": "qk_admission",
-        "pair_service_fraction": out["service"].view(B, H, 1, P),
-    }
+    routing_state.pop(_PV_SERVICE_PENDING, None)
+    if domain == "qk_admission":
+        routing_state[SERVICE_KEY] = {
+            "layer_idx": int(layer_idx),
+            "identity_observed": True,
+            "service_domain": "qk_admission",
+            "pair_service_fraction": out["service"].view(B, H, 1, P),
+        }
+    else:
+        routing_state[_PV_SERVICE_PENDING] = (int(layer_idx), out["service"].view(B, H, 1, P))
     if "priority" in out:
         routing_state["cosa_value_risk_pair_priority"] = out["priority"]
     routing_state["cosa_value_risk_pair_max_patch_blocks"] = int(M)
     routing_state["cosa_value_risk_pair_selected_indices"] = out["index"][..., :M]
     routing_state["cosa_value_risk_pair_qk_order_priority"] = score.float().clamp_min(0.0).nan_to_num(nan=0.0)
+
+
+def _record_pv_execution(routing_state: dict | None) -> None:
+    """PV-execution service of the layer just attended (SW:8055-8217 with
+    ``_reduce_exact_pv_execution_to_pair``, SW:2983-3028).
+
+    The PV threshold is inert (1e10; finite thresholds are rejected by
+    ``routing_config``), so every listed block runs its PV product in each of
+    the four 32-row query waves of its 128-row block: the execution map is
+    the selected support repeated over the waves. The exact reduction,
+    ``(4 * count) / (4 * Q * pair_size)``, divides the same integers as the
+    QK-admission fraction ``count / (Q * pair_size)`` written by the select
+    kernel, so the two are the same float32 values.
+    """
+    if routing_state is None:
+        return
+    pending = routing_state.pop(_PV_SERVICE_PENDING, None)
+    if pending is None:
+        return
+    layer_idx, service = pending
+    routing_state[SERVICE_KEY] = {
+        "layer_idx": int(layer_idx),
+        "identity_observed": True,
+        "pair_service_fraction": service,
+    }
 
 
 def _stats(out: dict, cap: torch.Tensor | None) -> dict:
@@ -240,7 +283,7 @@ def get_cosa_value_risk_pair_debt_mask(pooled_score: torch.Tensor, pooled_value:
     out = ops.select_blocks(pooled_score, mode=_lib.MODE_VASC, topk=0, innovation=innovation, row_cap=cap,
                             protected_mask=protected_mask, max_capacity=M, debt=debt, pending_arrival=pending,
                             prev_service=service, want_mask=True, want_priority=True)
-    _ledger_outputs(routing_state, out, pooled_score, layer_idx, M)
+    _ledger_outputs(routing_state, out, pooled_score, layer_idx, M, _service_domain())
     if stats_store is not None:
         stats_store.update(_stats(out, cap))
     return out["mask"].bool()
@@ -264,7 +307,7 @@ def finalize_cosa_value_risk_pair_debt(routing_state: dict | None, *, stats_stor
     if obs.get("layer_idx") != pending_layer:
         raise RuntimeError("terminal PV service does not match CoSA layer")
     if "pair_service_fraction" not in obs:
-        raise NotImplementedError("only the qk_admission service domain is built")
+        raise RuntimeError("PV service observation carries no pair service fraction")
     service = obs["pair_service_fraction"]
     prev = routing_state.get(STATE_KEY)
     if prev is not None and tuple(prev.shape) != tuple(pending.shape):
@@ -340,7 +383,7 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
                                 row_cap=base, force_last=force_last, max_capacity=hint, sink_blocks=sink, debt=debt,
                                 pending_arrival=pending, prev_service=service,
                                 want_priority=not cfg.skip_routing_stats)
-        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, min(hint, orig_kblk))
+        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, min(hint, orig_kblk), cfg.service_domain)
         if routing_stats_store is not None:
             routing_stats_store.update(_stats(sel, None))
     elif count is not None:
@@ -378,6 +421,7 @@ def block_sparse_attn_cuda(query: torch.Tensor, key: torch.Tensor, value: torch.
                                         routing_stats_store, routing_state, num_patch_tokens, research)
     vt = ops.pack_v(value)
     o = ops.block_sparse_attn(query, key, vt, sel["index"], sel["count"])
+    _record_pv_execution(routing_state)
     if o.dtype != query.dtype:
         o = o.to(query.dtype)
     if return_sparsity:
@@ -400,4 +444,5 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
                                         routing_stats_store, routing_state, num_patch_tokens, research)
     vt = ops.pack_v(value)
     o_patch, o_special = ops.global_attn(q_patch, q_special, key, vt, sel["index"], sel["count"])
+    _record_pv_execution(routing_state)
     return o_patch, o_special, _sparsity(sel, total_kblk)
