@@ -58,10 +58,11 @@ def test_pack_v_layout_bit_exact():
     assert torch.equal(vt.view(torch.int16), expect.contiguous().view(torch.int16))
 
 
-@pytest.mark.parametrize("nq,nk,seed", [(128, 64, 0), (300, 200, 1), (1000, 1041, 2), (77, 130, 3)])
-def test_block_sparse_matches_oracle(nq, nk, seed):
+@pytest.mark.parametrize("nq,nk,seed,B", [(128, 64, 0, 1), (300, 200, 1, 1), (1000, 1041, 2, 1), (77, 130, 3, 1),
+                                         (300, 330, 4, 2)])
+def test_block_sparse_matches_oracle(nq, nk, seed, B):
     from vasc_amd import ops
-    B, H, D = 1, 2, 64
+    H, D = 2, 64
     q, k, v = _rand((B, H, nq, D), seed), _rand((B, H, nk, D), seed + 100), _rand((B, H, nk, D), seed + 200)
     qb, nkb = math.ceil(nq / 128), math.ceil(nk / 64)
     idx, cnt = _lists(B, H, qb, nkb, seed)

@@ -25,10 +25,10 @@ def _bf16_close(gpu, ref):
     return float((gpu != ref).mean())
 
 
-@pytest.mark.parametrize("nq,nk", [(8288, 8288), (1000, 1041), (128, 64), (77, 130)])
-def test_pool_qkv_matches_oracle(nq, nk):
+@pytest.mark.parametrize("nq,nk,B", [(8288, 8288, 1), (1000, 1041, 1), (128, 64, 1), (77, 130, 1), (500, 640, 2)])
+def test_pool_qkv_matches_oracle(nq, nk, B):
     from vasc_amd import ops
-    B, H, D = 1, 3, 64
+    H, D = 3, 64
     q, k, v = _rand((B, H, nq, D), 1), _rand((B, H, nk, D), 2), _rand((B, H, nk, D), 3)
     pq, pk, pv, inn = ops.pool_qkv(q.cuda(), k.cuda(), v.cuda())
     diff_frac = [

@@ -103,19 +103,19 @@ def test_topk_signed_scores_bit_exact(K):
             _assert_lists(out, sel, 0)
 
 
-def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=False, levels=None):
+def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=False, levels=None, B=1):
     from vasc_amd import ops
     rng = np.random.default_rng(seed)
     st = {}
     debt = pending = service = None
     gates = []
     for layer in range(layers):
-        score = _scores(rng, (1, H, Q, K), peak=peak, levels=levels)
-        pv = rng.standard_normal((1, H, K, 64)).astype(np.float32)
+        score = _scores(rng, (B, H, Q, K), peak=peak, levels=levels)
+        pv = rng.standard_normal((B, H, K, 64)).astype(np.float32)
         iota = OS.innovation(pv)
         if row_caps:
-            cap = rng.integers(0, K + 1, (1, H, Q))
-            prot = np.zeros((1, H, Q, K), bool)
+            cap = rng.integers(0, K + 1, (B, H, Q))
+            prot = np.zeros((B, H, Q, K), bool)
             prot[..., -1] = cap > 0
             hint = None
             M = int(cap.max())
@@ -126,7 +126,7 @@ def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=
             cap = base.sum(-1)
             prot = None
             if force_last:
-                prot = np.zeros((1, H, Q, K), bool)
+                prot = np.zeros((B, H, Q, K), bool)
                 prot[..., K - 1] = True
             hint = topk + int(force_last)
             M = min(hint, K)
@@ -161,6 +161,12 @@ def test_vasc_chain_bit_exact(K, Q, force_last, peak, levels):
     topk = max(int(K * 0.25), 1)
     gates = _run_chain(K, Q, 4, 8, topk=topk, force_last=force_last, sink=1, peak=peak, seed=K, levels=levels)
     assert any(gates[1:]) or True  # gate activity is data dependent; parity is the assertion
+
+
+def test_vasc_chain_batch2_bit_exact():
+    """Two batch entries: per-(b, h) ledgers and the gate's sum over every
+    (b, h) head in order."""
+    _run_chain(518, 20, 3, 4, topk=129, force_last=True, sink=3, peak=2.0, seed=31, B=2)
 
 
 def test_vasc_row_caps_and_protected_bit_exact():
