@@ -49,22 +49,6 @@ struct PackParams {
   uint16_t *q_patch, *q_special, *k_out, *v_out;
 };
 
-// Cross-lane moves inside groups of 8 lanes by DPP: xor 1 and xor 2 are
-// quad permutations, and the half-row mirror (lane i <-> 7 - i) reaches the
-// other quad of the group.
-template <int kCtrl>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xf, 0xf, false));
-}
-constexpr int kQuadXor1 = 0xb1;   // quad_perm [1, 0, 3, 2]
-constexpr int kQuadXor2 = 0x4e;   // quad_perm [2, 3, 0, 1]
-constexpr int kHalfMirror = 0x141;
-
-__device__ __forceinline__ float group8_sum(float v) {
-  v += dpp<kQuadXor1>(v);
-  v += dpp<kQuadXor2>(v);
-  return v + dpp<kHalfMirror>(v);
-}
 
 // Workgroup (x, b): tensor/head th = x % 3H (0..H-1 q, H..2H-1 k, 2H..3H-1
 // v), tokens [64 (x / 3H), +64) of batch entry b; consecutive workgroups

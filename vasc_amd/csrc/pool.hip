@@ -2,8 +2,9 @@
 //
 // 1a (pool_qkv_kernel) is HBM-bound: each workgroup streams one 128-token
 // span of Q, K and V (3 x 16 KB) with 16-byte coalesced loads, reduces the
-// 8-lane groups that share a 16-byte column with xor shuffles and the four
-// waves through LDS, and writes one pooled Q row, two pooled K rows and two
+// 8-lane groups that share a 16-byte column with DPP moves (no LDS traffic)
+// and the four waves through LDS, and writes one pooled Q row, two pooled K
+// rows and two
 // pooled V rows (bf16, as avg_pool1d on bf16 input produces), plus the
 // innovation of the V pair it just pooled, so the value-contrast score needs
 // no second pass over V. Algorithmic traffic: 3*2*d bytes per token read,
@@ -45,7 +46,10 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int dc = tid & 7, r = tid >> 3;
+  // lane bits 0-2: token within a group of 8, bits 3-5: 16-byte feature
+  // chunk; a load instruction still covers 8 whole 128-byte rows, and the
+  // token reduction stays inside DPP groups of 8 lanes
+  const int t8 = lane & 7, dc = lane >> 3;
 
   // Issue all 12 row loads (3 tensors x 4 rows) before any reduction so each
   // thread keeps 192 bytes in flight.
@@ -55,7 +59,7 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
     const uint16_t *src = p.x[X] ? p.x[X] + b * p.sb[X] + h * p.sh[X] + dc * 8 : nullptr;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int64_t tok = chunk * 128 + r + 32 * u;
+      const int64_t tok = chunk * 128 + 32 * u + 8 * w + t8;
       raw[X][u] = (src && tok < p.ntok[X]) ? *reinterpret_cast<const u32x4 *>(src + tok * p.st[X])
                                            : u32x4{0, 0, 0, 0};
     }
@@ -79,14 +83,8 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
 #pragma unroll
     for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float s = acc[half][i];
-        s += __shfl_xor(s, 8);
-        s += __shfl_xor(s, 16);
-        s += __shfl_xor(s, 32);
-        acc[half][i] = s;
-      }
-    if (lane < 8) {
+      for (int i = 0; i < 8; ++i) acc[half][i] = group8_sum(acc[half][i]);
+    if (t8 == 0) {
 #pragma unroll
       for (int half = 0; half < 2; ++half)
 #pragma unroll
