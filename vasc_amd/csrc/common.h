@@ -99,13 +99,54 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
 }
 
+// The value of lane (lane ^ off) for off in {1, 2, 4, 8, 16, 32}, by VALU
+// cross-lane moves instead of an LDS permute: DPP quad permutations (1, 2),
+// row shifts selected by lane bit 2 (4), a row rotate by 8 (8), and gfx950's
+// v_permlane16_swap / v_permlane32_swap, which exchange rows of 16 / 32
+// lanes (16, 32). `off` must be a constant after unrolling.
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int off) {
+  const int lane = __lane_id();
+  switch (off) {
+    case 1: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xb1, 0xf, 0xf, false));
+    case 2: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4e, 0xf, 0xf, false));
+    case 4: {
+      const uint32_t up = __builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x104, 0xf, 0xf, false);  // row_shl:4
+      const uint32_t dn = __builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x114, 0xf, 0xf, false);  // row_shr:4
+      return (lane & 4) ? dn : up;
+    }
+    case 8: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x128, 0xf, 0xf, false));
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return (lane & 16) ? r[0] : r[1];
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return (lane & 32) ? r[0] : r[1];
+    }
+  }
+}
+__device__ __forceinline__ int xor_lane(int v, int off) {
+  return static_cast<int>(xor_lane(static_cast<uint32_t>(v), off));
+}
+__device__ __forceinline__ float xor_lane(float v, int off) {
+  return __uint_as_float(xor_lane(__float_as_uint(v), off));
+}
+__device__ __forceinline__ double xor_lane(double v, int off) {
+  const uint64_t u = __double_as_longlong(v);
+  const uint64_t lo = xor_lane(static_cast<uint32_t>(u), off), hi = xor_lane(static_cast<uint32_t>(u >> 32), off);
+  return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
+}
+
 // Canonical 64-lane xor butterfly of float64 lane sums (offsets 32..1).
 __device__ __forceinline__ double wave_butterfly(double s) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off);
+  for (int off = 32; off >= 1; off >>= 1) s = s + xor_lane(s, off);
   return s;
 }
 
+// Integer and max reductions keep the LDS permute: the kernels that use them
+// are VALU-bound, and one ds_bpermute per stage costs them less than the
+// VALU moves.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
