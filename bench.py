@@ -372,7 +372,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the sparse op shards by head; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the sparse op would shard by head, one head group per GPU). Run with --gpus 1.", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
