@@ -219,6 +219,33 @@ int vasc_block_sparse_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
                                void *stream);
 
 /*
+ * vasc_block_sparse_attn_fwd with the PV post-cut of the reference's
+ * qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
+ * (ZIP:csrc/qattn/qk_int_sv_f16_cuda_sm80.cu:188-376, per-block mode;
+ * skip branch qk_int_sv_f16_cuda_sm80.cuh:291-381, update_mo
+ * attn_utils.cuh:419-466) and its return_pv_count map. Per 128-row query
+ * block and listed key block: gap = max over rows of (block row max -
+ * running row max), log2 units (logit * sm_scale * log2 e); the running max
+ * starts at -5e6 and follows every listed block; the block's exp, row sum and
+ * PV run only when gap + pv_threshold[h] > 0.
+ *
+ * pv_threshold  [H] float32 device array (log2 units).
+ * pv_map        optional [B,H,ceil(nq/128)*4,ceil(nk/64)] int32, zeroed by
+ *               the caller: 1 where a 32-row query wave ran a block's PV.
+ */
+int vasc_block_sparse_attn_pv_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
+                                  int64_t q_st, const uint16_t *k, int64_t k_sb,
+                                  int64_t k_sh, int64_t k_st, const uint16_t *vt,
+                                  uint16_t *o, int64_t o_sb, int64_t o_sh,
+                                  int64_t o_st, int64_t B, int64_t H, int64_t nq,
+                                  int64_t nk, int64_t d,
+                                  const int32_t *block_index, int64_t index_width,
+                                  const int32_t *block_count,
+                                  int32_t index_is_delta, float sm_scale,
+                                  const float *pv_threshold, int32_t *pv_map,
+                                  void *stream);
+
+/*
  * Kernel 4 for a whole global layer: the patch queries q_patch [B,H,n_patch,d]
  * attend to their listed blocks as in vasc_block_sparse_attn_fwd (absolute
  * indices), and the special-token queries q_special [B,H,n_special,d] attend

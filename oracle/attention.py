@@ -12,11 +12,16 @@ detail); rows beyond the query end are not written. The reference kernel
 quantises Q/K to int8 and P to fp16; this oracle is the exact float64
 computation that both the reference and the bf16 HIP kernel approximate.
 
-Pinning: ``tests/test_oracle_attention.py`` checks it against
+Pinning: ``tests/test_oracle_misc.py`` checks it against
 ``torch.nn.functional.scaled_dot_product_attention`` with a dense boolean
 mask in float64, and that full index lists reproduce dense attention.
+``pv_post_cut`` (the PV threshold) is pinned by hand-computed decision
+sequences on rank-one logits, the strict ``gap + threshold > 0`` boundary,
+the inert 1e10 threshold and the zero logits of padded query rows.
 """
 from __future__ import annotations
+
+import math
 
 import numpy as np
 
@@ -52,6 +57,55 @@ def block_sparse_attention(q, k, v, index_lists, counts, *, block_q: int = 128,
                 p /= p.sum(axis=-1, keepdims=True)
                 out[b, h, rows] = p @ v[b, h, keys]
     return out
+
+
+def pv_post_cut(q, k, index_lists, counts, pv_threshold, *, block_q: int = 128, block_k: int = 64,
+                scale: float | None = None, waves: int = 4):
+    """The PV post-cut's decisions (qk_int_sv_f16_cuda_sm80.cuh:291-381 with
+    update_mo, attn_utils.cuh:419-466, per-block mode).
+
+    For each query block, over its listed key blocks in list order: the
+    block row max ``max(-5e6, max_key logit) * scale * log2 e`` (query rows
+    past ``Nq`` count with zero logits), gap = max over the block's rows of
+    (block row max - running row max), running max (from -5e6) raised to the
+    block row max whether or not PV runs. PV runs when gap + threshold > 0.
+
+    Returns ``(lists, counts, pv_map)``: the executed blocks (list order) and
+    the int32 map ``[B, H, Qb*waves, Kb]`` with 1 where each query wave ran
+    PV. Attention over the executed lists (``block_sparse_attention``) is the
+    post-cut output: a skipped block adds to neither numerator nor sum.
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    B, H, Nq, D = q.shape
+    Tk = k.shape[-2]
+    Kb = -(-Tk // block_k)
+    scale = D ** -0.5 if scale is None else scale
+    c = scale * math.log2(math.e)
+    thr = np.broadcast_to(np.asarray(pv_threshold, np.float64).reshape(-1), (H,))
+    Qb = -(-Nq // block_q)
+    W = index_lists.shape[-1]
+    lists = np.full((B, H, Qb, W), -1, np.int32)
+    cnt = np.zeros((B, H, Qb), np.int32)
+    pv_map = np.zeros((B, H, Qb * waves, Kb), np.int32)
+    for b in range(B):
+        for h in range(H):
+            for i in range(Qb):
+                rows = np.zeros((block_q, D))
+                r1 = min((i + 1) * block_q, Nq)
+                rows[: r1 - i * block_q] = q[b, h, i * block_q: r1]
+                run = np.full(block_q, -5e6)
+                for blk in np.asarray(index_lists[b, h, i, : int(counts[b, h, i])], np.int64):
+                    keys = blk * block_k + np.arange(block_k)
+                    keys = keys[keys < Tk]
+                    bm = np.maximum(-5e6, (rows @ k[b, h, keys].T).max(axis=-1)) * c
+                    gap = (bm - run).max()
+                    run = np.maximum(run, bm)
+                    if gap + thr[h] > 0:
+                        lists[b, h, i, cnt[b, h, i]] = blk
+                        cnt[b, h, i] += 1
+                        pv_map[b, h, i * waves:(i + 1) * waves, blk] = 1
+    return lists, cnt, pv_map
 
 
 def dense_lists(B: int, H: int, Nq: int, Tk: int, block_q: int = 128, block_k: int = 64):

@@ -248,6 +248,57 @@ def test_pv_execution_service_domain_chain(release_env):
     assert SW.finalize_cosa_value_risk_pair_debt(st_gpu)
 
 
+def test_pv_post_cut_service_through_block_sparse_attn(release_env, monkeypatch):
+    """A finite PV threshold (natural_gap, 6 log2 units) in vasc mode with the
+    PV-execution domain, on graded data (every key block's logits sit at a
+    multiple of 4 log2 units, so no decision is near the threshold): the
+    kernel's execution map equals the oracle's decisions on the lists
+    block_sparse_attn_cuda launched, and the observed service is the oracle's
+    exact reduction of that map, bit for bit, over two chained layers."""
+    from vasc_amd import ops
+    from vasc_amd import sparse_wrapper as SW
+    from vasc_amd.attention import predict_attention
+    release_env("pi3", "vasc")
+    os.environ["SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN"] = "pv_execution"
+    os.environ["SPARSE_VGGT_QK_PV_THRESHOLD"] = f"natural_gap:{6.0 / math.log2(math.e)!r}"
+    captured = {}
+    launch = ops.block_sparse_attn_pv
+
+    def spy(q, k, vt, index, count, thr, **kw):
+        o, m = launch(q, k, vt, index, count, thr, **kw)
+        captured.update(index=index.cpu().numpy(), count=count.cpu().numpy(), thr=thr, map=m.cpu().numpy())
+        return o, m
+
+    monkeypatch.setattr(ops, "block_sparse_attn_pv", spy)
+    N, P, S, H, D = 4, 1041, 5, 4, 64
+    Np, Tk = N * (P - S), N * P
+    c = D ** -0.5 * math.log2(math.e)
+    rng = np.random.default_rng(12)
+    st = {}
+    for layer in range(2):
+        q = torch.from_numpy(rng.standard_normal((1, H, Np, D)) * 0.01).float()
+        q[..., 0] += 1.0
+        k = torch.from_numpy(rng.standard_normal((1, H, Tk, D)) * 0.01).float()
+        lv = rng.choice([0.0, 4.0, 8.0, 12.0], size=(1, H, math.ceil(Tk / 64)))
+        k[..., 0] += torch.from_numpy(np.repeat(lv, 64, axis=-1)[..., :Tk] / c).float()
+        v = torch.from_numpy(rng.standard_normal((1, H, Tk, D))).float()
+        q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+        qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+        score = predict_attention(qc, kc[:, :, :Np])
+        SW.block_sparse_attn_cuda(qc, kc, vc, score, sparse_ratio=0.75, layer_idx=layer, routing_state=st,
+                                  num_patch_tokens=Np)
+        assert abs(captured["thr"] - 6.0) < 1e-9
+        _, _, ref_map = OA.pv_post_cut(q.float().numpy(), k.float().numpy(), captured["index"],
+                                       captured["count"], 6.0)
+        assert np.array_equal(captured["map"], ref_map), layer
+        assert ref_map.sum() < 4 * captured["count"].sum()  # the cut skipped blocks
+        Kb = score.shape[-1]
+        ref = OS.pv_execution_service(ref_map.reshape(1, H, -1, 4, ref_map.shape[-1]), Kb)
+        obs = st[SW.SERVICE_KEY]
+        assert np.array_equal(_bits(obs["pair_service_fraction"][:, :, 0]), ref.view(np.uint32)), layer
+    assert SW.finalize_cosa_value_risk_pair_debt(st)
+
+
 def test_global_layer_forward_dense_limit():
     """adaptive_sparse_attention_forward at sparsity 0 equals dense attention of
     the same module (all key blocks kept)."""

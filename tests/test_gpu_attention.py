@@ -190,3 +190,38 @@ def test_extreme_logits_take_the_exact_path(case):
     dense = ops.dense_attn(q.cuda(), k.cuda(), ops.pack_v(v.cuda()))
     dl = OA.dense_lists(B, H, nq, nk)
     _check(dense, OA.block_sparse_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), *dl))
+
+
+# ---------------------------------------------------------------- PV post-cut
+def _graded_blocks(nq, nk, levels, seed):
+    """Query rows a*e0 (+ small noise) and key block j = levels[j] / c * e0
+    (+ small noise): block j's logits sit at levels[j] in log2 units, so the
+    post-cut decisions have margins of whole log2 units."""
+    D = 64
+    c = D ** -0.5 * math.log2(math.e)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, 2, nq, D, generator=g) * 0.01
+    q[..., 0] += 1.0
+    k = torch.randn(1, 2, nk, D, generator=g) * 0.01
+    for j in range(math.ceil(nk / 64)):
+        k[:, :, 64 * j:64 * (j + 1), 0] += float(levels[j % len(levels)]) / c
+    v = torch.randn(1, 2, nk, D, generator=g)
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("nq,nk,thr", [(512, 1000, 6.0), (300, 1041, 6.0), (256, 640, [6.0, 1e10])])
+def test_pv_post_cut_matches_oracle(nq, nk, thr):
+    """Execution map bit-exact with the oracle's decisions; output within
+    tolerance of float64 attention over the executed blocks."""
+    from vasc_amd import ops
+    levels = [0, 8, 4, 12, 0, 4, 8, 0]  # log2 units; with threshold 6 every gap + 6 is >= 2 away from 0
+    q, k, v = _graded_blocks(nq, nk, levels, seed=nq)
+    qb, nkb = math.ceil(nq / 128), math.ceil(nk / 64)
+    idx, cnt = _lists(1, 2, qb, nkb, seed=nk, density=0.6)
+    o, pv_map = ops.block_sparse_attn_pv(q.cuda(), k.cuda(), ops.pack_v(v.cuda()), torch.from_numpy(idx).cuda(),
+                                         torch.from_numpy(cnt).cuda(), thr)
+    ex_idx, ex_cnt, ref_map = OA.pv_post_cut(q.float().numpy(), k.float().numpy(), idx, cnt, thr)
+    assert ref_map.sum() < 4 * cnt.sum()  # the cut removed blocks
+    assert np.array_equal(pv_map.cpu().numpy(), ref_map)
+    ref = OA.block_sparse_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), ex_idx, ex_cnt)
+    _check(o, ref)

@@ -43,12 +43,28 @@ def test_routing_config_resolves_release_modes():
 
 def test_routing_config_rejects_research_switches():
     env = launcher.method_environment("vggt", "vasc")
-    for extra in ({"SPARSE_VGGT_COSA_ORDERED_LUT": "1"}, {"SPARSE_VGGT_QK_PV_THRESHOLD": "sequence_mass_bound"},
-                  {"SPARSE_VGGT_QK_PV_THRESHOLD": "4.0", "SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN": "pv_execution"}):
+    for extra in ({"SPARSE_VGGT_COSA_ORDERED_LUT": "1"}, {"SPARSE_VGGT_RADIAL_A_DENSE": "1"}):
         with pytest.raises(NotImplementedError):
             launcher.routing_config({**env, **extra})
+    for bad in ("-1", "natural_gap:-2", "nan", "abc"):  # as _resolve_qk_pv_threshold (SW:3064-3087)
+        with pytest.raises(ValueError):
+            launcher.routing_config({**env, "SPARSE_VGGT_QK_PV_THRESHOLD": bad})
     with pytest.raises(ValueError):  # as the reference selector (SW:3999-4000)
         launcher.routing_config({**env, "SPARSE_VGGT_COSA_DEBT_SERVICE_DOMAIN": "pv_count"})
+
+
+def test_pv_threshold_resolution():
+    import math
+    assert launcher.resolve_pv_threshold("sequence_mass_bound", 33312) == math.log(33312.0)
+    assert launcher.resolve_pv_threshold("sequence_mass_bound", 1) == math.log(2.0)
+    assert launcher.resolve_pv_threshold("natural_gap:2", 10) == 2 * math.log2(math.e)
+    assert launcher.resolve_pv_threshold("1e10", 10) == 1e10
+    assert launcher.pv_threshold_active("", 5) and launcher.pv_threshold_active(" 0, 7,15 ", 7)
+    assert not launcher.pv_threshold_active("0,7,15", 8)
+    env = {**launcher.method_environment("pi3", "vasc"), "SPARSE_VGGT_QK_PV_THRESHOLD": "sequence_mass_bound",
+           "SPARSE_VGGT_QK_PV_ACTIVE_LAYERS": "1,3"}
+    cfg = launcher.routing_config(env)
+    assert cfg.pv_threshold == "sequence_mass_bound" and cfg.pv_active_layers == "1,3"
 
 
 def test_routing_config_service_domains():
@@ -82,7 +98,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES), "ctypes table out of sync with include/vasc_hip.h"
-    assert lib.vasc_abi_version() == 3
+    assert lib.vasc_abi_version() == 4
 
 
 def test_host_only_queries_and_argument_errors():
@@ -134,3 +150,6 @@ def test_host_only_queries_and_argument_errors():
     assert rc == 2 and b"8192" in lib.vasc_last_error()
     rc = lib.vasc_cdf_counts(fake, 1, 16, 259, 518, fake, 519, 0, fake, None, None)
     assert rc == 1 and b"min_count" in lib.vasc_last_error()
+    rc = lib.vasc_block_sparse_attn_pv_fwd(None, 0, 0, 8, None, 0, 0, 8, None, None, 0, 0, 8, 1, 1, 128, 64, 64,
+                                           None, 1, None, 0, ctypes.c_float(0.125), None, None, None)
+    assert rc == 1 and b"pv_threshold" in lib.vasc_last_error()

@@ -124,3 +124,55 @@ def test_cpu_baseline_matches_float64_oracle():
     idx, cnt = OS.index_lists(final)
     ref = OA.block_sparse_attention(q.double().numpy(), k.double().numpy(), v.double().numpy(), idx, cnt)
     np.testing.assert_allclose(out.numpy(), ref, atol=2e-5)
+
+
+# ---------------------------------------------------------------- PV post-cut
+def _rank_one(levels, Nq=128, block_k=64, a=1.0):
+    """q rows = a * e0, key block j = levels[j] * e0: every logit of block j
+    is a * levels[j], so block j's row max is a * levels[j] * D^-0.5 * log2 e."""
+    D = 64
+    q = np.zeros((1, 1, Nq, D))
+    q[..., 0] = a
+    k = np.zeros((1, 1, len(levels) * block_k, D))
+    for j, lv in enumerate(levels):
+        k[0, 0, j * block_k:(j + 1) * block_k, 0] = lv
+    return q, k
+
+
+def _unit():
+    return 64 ** -0.5 * np.log2(np.e)  # log2 units per unit logit
+
+
+def test_pv_post_cut_hand_sequences():
+    u = _unit()
+    # logits 10, 0, 5 (in units of 1/u) with threshold 6: the first block always runs,
+    # 0 is 10 below the running max (skip), 5 is 5 below (runs: -5 + 6 > 0)
+    q, k = _rank_one([10 / u, 0.0, 5 / u])
+    idx = np.array([[[[0, 1, 2]]]], np.int32)
+    lists, cnt, m = OA.pv_post_cut(q, k, idx, np.array([[[3]]]), 6.0)
+    assert cnt[0, 0, 0] == 2 and list(lists[0, 0, 0, :2]) == [0, 2]
+    assert m[0, 0, :4, 0].all() and not m[0, 0, :, 1].any() and m[0, 0, :4, 2].all()
+    # increasing maxima always run; a later low block is judged against the raised max
+    q, k = _rank_one([0.0, 10 / u, 3 / u])
+    lists, cnt, _ = OA.pv_post_cut(q, k, idx, np.array([[[3]]]), 6.0)
+    assert list(lists[0, 0, 0, : cnt[0, 0, 0]]) == [0, 1]
+    # list order, not block order: listed as 1, 0, 2 the highest block comes first and
+    # both others fall more than 6 below it
+    lists, cnt, _ = OA.pv_post_cut(q, k, np.array([[[[1, 0, 2]]]], np.int32), np.array([[[3]]]), 6.0)
+    assert list(lists[0, 0, 0, : cnt[0, 0, 0]]) == [1]
+
+
+def test_pv_post_cut_boundary_inert_and_padded_rows():
+    u = _unit()
+    q, k = _rank_one([8 / u, 2 / u])
+    idx, c1 = np.array([[[[0, 1]]]], np.int32), np.array([[[2]]])
+    assert OA.pv_post_cut(q, k, idx, c1, 6.0)[1][0, 0, 0] == 1           # gap -6 + 6 = 0: skipped
+    assert OA.pv_post_cut(q, k, idx, c1, 6.0 + 1e-9)[1][0, 0, 0] == 2    # just above: runs
+    lists, cnt, m = OA.pv_post_cut(q, k, idx, c1, 1e10)
+    assert cnt[0, 0, 0] == 2 and m.sum() == 8
+    # query rows past Nq count with zero logits: with all real logits negative,
+    # the zero rows set the block maxima
+    q, k = _rank_one([-50 / u, -60 / u], Nq=100, a=1.0)
+    assert OA.pv_post_cut(q, k, idx, c1, 1.0)[1][0, 0, 0] == 2           # padded rows: 0 and 0, gap 0
+    q, k = _rank_one([-50 / u, -60 / u], Nq=128, a=1.0)
+    assert OA.pv_post_cut(q, k, idx, c1, 1.0)[1][0, 0, 0] == 1           # no padding: gap -10

@@ -39,6 +39,8 @@ SIGNATURES: dict[str, tuple] = {
     "vasc_pack_v": (c_int32, [P, I64, I64, I64, I64, I64, I64, I64, P, P]),
     "vasc_block_sparse_attn_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, P, I64, I64, I64,
                                              I64, I64, I64, I64, I64, P, I64, P, I32, c_float, P]),
+    "vasc_block_sparse_attn_pv_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, P, I64, I64, I64,
+                                                I64, I64, I64, I64, I64, P, I64, P, I32, c_float, P, P, P]),
     "vasc_dense_attn_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, P, I64, I64, I64,
                                       I64, I64, I64, I64, I64, c_float, P]),
     "vasc_global_attn_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64, P,

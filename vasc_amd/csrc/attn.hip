@@ -70,6 +70,11 @@ struct AttnParams {
   uint16_t *o2;
   int64_t o2_sb, o2_sh, o2_st;
   int64_t nq2, nq2b, num_wg2;
+  // PV post-cut (kPv instances): per-head thresholds in log2 units and the
+  // per-wave execution map [B, H, nqb * 4, pv_w] (written where PV ran)
+  const float *pv_thr;
+  int32_t *pv_map;
+  int64_t pv_w;
 };
 
 __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
@@ -92,11 +97,12 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 constexpr float kHigh = 18446744073709551616.0f;  // 2^64
 constexpr float kLow = 8.673617379884035e-19f;    // 2^-60
 
-template <bool kDense>
+template <bool kDense, bool kPv = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void bsattn_fwd_kernel(const AttnParams p) {
   constexpr int CH = 512 / kThreads;  // 16-byte chunks per thread per tile
   __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][kTile];  // [buffer][K, Vt]
+  __shared__ float pv_gap[kPv ? 4 : 1];                                 // per-wave gap of the PV post-cut
   auto lds_u32 = [](const uint16_t *ptr) { return lds_addr32(ptr); };
 
   // Workgroups [0, num_wg2) take the special-token queries (every key
@@ -196,6 +202,8 @@ void bsattn_fwd_kernel(const AttnParams p) {
   float ls = 0.f;  // running sum of the bf16 probabilities (this lane's 32 keys per block)
   float m = 0.f;   // exponent offset of this lane's row (log2 units)
   const float c = p.c;
+  float run_max = -5000000.0f;  // PV post-cut: running row max (log2 units)
+  const float pv_threshold = kPv ? p.pv_thr[h] : 0.f;
 
   // P = exp2(c S - m) for k-step s of the PV product (accumulators
   // 8(s%2)..+7 of tile s/2), packed to bf16; returns bs plus the sum of the
@@ -294,6 +302,34 @@ void bsattn_fwd_kernel(const AttnParams p) {
         S[t] = mfma32(a, qf[s], s == 0 ? zero16 : S[t]);
       }
 
+    // PV post-cut (qk_int_sv_f16_cuda_sm80.cuh:291-381 with update_mo,
+    // attn_utils.cuh:419-466, per-block mode): gap = the largest over the
+    // workgroup's rows of (block row max - running max) in log2 units; the
+    // running max starts at -5e6 and follows every listed block, executed or
+    // not; PV runs for the whole workgroup only when gap + threshold > 0.
+    if constexpr (kPv) {
+      if (!dense) {
+        const int lim = valid_keys(cur);
+        float mx = -5000000.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int kk = 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
+            mx = kk < lim ? fmaxf(mx, S[t][r]) : mx;
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+        const float gap = wave_max(mx - run_max);
+        run_max = fmaxf(run_max, mx);
+        if (l == 0) pv_gap[w] = gap;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const float g4 = fmaxf(fmaxf(pv_gap[0], pv_gap[1]), fmaxf(pv_gap[2], pv_gap[3]));
+        if (!(g4 + pv_threshold > 0.f)) continue;  // skipped: no P, no sum, no PV
+        if (l == 0 && p.pv_map && cur >= 0 && cur < nkb32)
+          p.pv_map[((bh * p.nqb + qb) * 4 + w) * p.pv_w + cur] = 1;
+      }
+    }
+
     u32x4 pb[4];
     float bs = exp_block(S, pb);
     const int lim = valid_keys(cur);
@@ -349,7 +385,8 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
                 uint16_t *o, int64_t o_sb, int64_t o_sh, int64_t o_st, int64_t B, int64_t H,
                 int64_t nq, int64_t nk, int64_t d, const int32_t *idx, int64_t idx_w,
                 const int32_t *cnt, int32_t delta, float sm_scale, void *stream,
-                const SpecialQueries &sq = SpecialQueries()) {
+                const SpecialQueries &sq = SpecialQueries(), const float *pv_thr = nullptr,
+                int32_t *pv_map = nullptr) {
   VASC_SUPPORTED(d == kHeadDim, "head_dim %lld not built (built: 64)", (long long)d);
   VASC_REQUIRE(B > 0 && H > 0 && nq > 0 && nk > 0, "sizes must be positive");
   int rc;
@@ -381,8 +418,11 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
   VASC_REQUIRE(p.num_wg + p.num_wg2 < (int64_t(1) << 31), "grid too large");
   VASC_SUPPORTED(nk < (int64_t(1) << 30) && nq < (int64_t(1) << 40), "sequence of %lld keys not built (< 2^30)",
                  (long long)nk);
+  p.pv_thr = pv_thr;
+  p.pv_map = pv_map;
+  p.pv_w = p.nkb;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  auto kern = dense ? bsattn_fwd_kernel<true> : bsattn_fwd_kernel<false>;
+  auto kern = dense ? bsattn_fwd_kernel<true> : (pv_thr ? bsattn_fwd_kernel<false, true> : bsattn_fwd_kernel<false>);
   hipLaunchKernelGGL(kern, dim3(p.num_wg + p.num_wg2), dim3(kThreads), 0, s, p);
   return check_launch(dense ? "vasc_dense_attn_fwd" : "vasc_block_sparse_attn_fwd");
 }
@@ -400,6 +440,19 @@ extern "C" int vasc_block_sparse_attn_fwd(const uint16_t *q, int64_t q_sb, int64
   return vasc::launch_attn(false, q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, vt, o, o_sb, o_sh, o_st, B, H,
                            nq, nk, d, block_index, index_width, block_count, index_is_delta, sm_scale,
                            stream);
+}
+
+extern "C" int vasc_block_sparse_attn_pv_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                                             const uint16_t *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                             const uint16_t *vt, uint16_t *o, int64_t o_sb, int64_t o_sh,
+                                             int64_t o_st, int64_t B, int64_t H, int64_t nq, int64_t nk,
+                                             int64_t d, const int32_t *block_index, int64_t index_width,
+                                             const int32_t *block_count, int32_t index_is_delta, float sm_scale,
+                                             const float *pv_threshold, int32_t *pv_map, void *stream) {
+  VASC_REQUIRE(pv_threshold != nullptr, "pv_threshold ([H] float32, device) is required");
+  return vasc::launch_attn(false, q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, vt, o, o_sb, o_sh, o_st, B, H,
+                           nq, nk, d, block_index, index_width, block_count, index_is_delta, sm_scale, stream,
+                           vasc::SpecialQueries(), pv_threshold, pv_map);
 }
 
 extern "C" int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st,

@@ -10,6 +10,7 @@ the reference's environment keep working.
 """
 from __future__ import annotations
 
+import math
 import os
 from dataclasses import dataclass
 
@@ -112,6 +113,8 @@ class RoutingConfig:
     official_mask: bool = False  # VGGT: no forced/protected mixed-tail block
     skip_routing_stats: bool = True
     service_domain: str = "qk_admission"  # ledger service: "qk_admission" or "pv_execution"
+    pv_threshold: str = "1e10"   # SPARSE_VGGT_QK_PV_THRESHOLD (resolved per layer)
+    pv_active_layers: str = ""   # SPARSE_VGGT_QK_PV_ACTIVE_LAYERS (empty: every layer)
 
 
 def routing_config(env=None) -> RoutingConfig:
@@ -139,12 +142,41 @@ def routing_config(env=None) -> RoutingConfig:
         if not _flag(env, "COSA_CONSERVATIVE_DEBT_PROJECTION"):
             unsupported.append("COSA_CONSERVATIVE_DEBT_PROJECTION=0")
     threshold = env.get("SPARSE_VGGT_QK_PV_THRESHOLD", "1e10")
-    try:
-        if float(threshold) < 1e10:
-            unsupported.append(f"QK_PV_THRESHOLD={threshold}")
-    except ValueError:
-        unsupported.append(f"QK_PV_THRESHOLD={threshold}")
+    if threshold != "sequence_mass_bound":
+        try:
+            resolve_pv_threshold(threshold, 2)
+        except ValueError as exc:
+            raise ValueError(str(exc)) from None
     if unsupported:
         raise NotImplementedError("switches outside the release modes: " + ", ".join(unsupported))
     return RoutingConfig(mode="vasc" if vasc else "topk", official_mask=_flag(env, "OFFICIAL_MASK"),
-                         skip_routing_stats=_flag(env, "SKIP_ROUTING_STATS"), service_domain=domain)
+                         skip_routing_stats=_flag(env, "SKIP_ROUTING_STATS"), service_domain=domain,
+                         pv_threshold=threshold, pv_active_layers=env.get("SPARSE_VGGT_QK_PV_ACTIVE_LAYERS", ""))
+
+
+def resolve_pv_threshold(spec: str, key_tokens: int) -> float:
+    """The PV post-cut threshold in log2 score units (SW:3064-3087):
+    ``sequence_mass_bound`` -> ln(max(N, 2)); ``natural_gap:x`` -> x * log2 e;
+    otherwise a non-negative number."""
+    if key_tokens <= 0:
+        raise ValueError("key token count must be positive")
+    if spec == "sequence_mass_bound":
+        return math.log(float(max(key_tokens, 2)))
+    if spec.startswith("natural_gap:"):
+        gap = float(spec.split(":", 1)[1])
+        if not math.isfinite(gap) or gap < 0.0:
+            raise ValueError("natural-logit PV gap must be finite and non-negative")
+        return gap * math.log2(math.e)
+    value = float(spec)
+    if not math.isfinite(value) or value < 0.0:
+        raise ValueError("SPARSE_VGGT_QK_PV_THRESHOLD must be non-negative or sequence_mass_bound")
+    return value
+
+
+def pv_threshold_active(spec: str, layer_idx: int) -> bool:
+    """Whether the PV post-cut runs at this global layer (SW:3090-3101):
+    every layer when ``spec`` is empty, else the listed layer indices."""
+    spec = spec.strip()
+    if not spec:
+        return True
+    return layer_idx in {int(t.strip()) for t in spec.split(",") if t.strip()}

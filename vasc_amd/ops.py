@@ -235,6 +235,37 @@ def block_sparse_attn(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, index:
     return o
 
 
+def block_sparse_attn_pv(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, index: torch.Tensor,
+                         count: torch.Tensor, pv_threshold, *, scale: float | None = None, delta: bool = False):
+    """``block_sparse_attn`` with the PV post-cut; ``pv_threshold`` is a
+    number or ``H`` values in log2 units. Returns ``(o, pv_map)`` with the
+    int32 execution map ``[B, H, ceil(Nq/128)*4, ceil(Nk/64)]``."""
+    q = _bhtd(q, "q")
+    k = _bhtd(k, "k")
+    _dev(vt, "vt")
+    B, H, nq, D = q.shape
+    nk = k.shape[2]
+    if vt.shape != (B, H, math.ceil(nk / BLOCK_K), D, BLOCK_K):
+        raise ValueError(f"vt shape {tuple(vt.shape)} does not match K {tuple(k.shape)}")
+    qb, kb = math.ceil(nq / BLOCK_Q), math.ceil(nk / BLOCK_K)
+    index = index.to(torch.int32).contiguous()
+    count = count.to(torch.int32).contiguous()
+    if index.shape[:3] != (B, H, qb) or count.shape != (B, H, qb):
+        raise ValueError(f"index/count must be [B,H,{qb},W]/[B,H,{qb}]")
+    thr = torch.as_tensor(pv_threshold, dtype=torch.float32).reshape(-1)
+    thr = (thr.expand(H) if thr.numel() == 1 else thr).contiguous().to(q.device)
+    if thr.numel() != H:
+        raise ValueError(f"pv_threshold must be a number or hold {H} values")
+    o = torch.empty(B, H, nq, D, device=q.device, dtype=torch.bfloat16)
+    pv_map = torch.zeros(B, H, qb * 4, kb, device=q.device, dtype=torch.int32)
+    scale = D ** -0.5 if scale is None else scale
+    _lib.call("vasc_block_sparse_attn_pv_fwd", q.data_ptr(), *q.stride()[:3], k.data_ptr(), *k.stride()[:3],
+              vt.data_ptr(), o.data_ptr(), *o.stride()[:3], B, H, nq, nk, D, index.data_ptr(),
+              index.shape[-1], count.data_ptr(), int(bool(delta)), float(scale), thr.data_ptr(),
+              pv_map.data_ptr(), _stream())
+    return o, pv_map
+
+
 def dense_attn(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, *, scale: float | None = None,
                out: torch.Tensor | None = None) -> torch.Tensor:
     """Dense attention with the same MFMA kernel (every key block)."""

@@ -29,7 +29,7 @@ import os
 import torch
 
 from . import _lib, ops
-from .launcher import routing_config
+from .launcher import pv_threshold_active, resolve_pv_threshold, routing_config
 
 KBLK = 64
 STATE_KEY = "cosa_value_risk_pair_debt"
@@ -189,17 +189,36 @@ def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_i
     routing_state["cosa_value_risk_pair_qk_order_priority"] = score.float().clamp_min(0.0).nan_to_num(nan=0.0)
 
 
-def _record_pv_execution(routing_state: dict | None) -> None:
+def _pv_execution_service(pv_map: torch.Tensor, patch_blocks: int) -> torch.Tensor:
+    """``_reduce_exact_pv_execution_to_pair`` (SW:2983-3028) of the kernel's
+    execution map ``[B, H, Qb*4, Kb]``: executed children per pair summed over
+    query blocks, waves and the pair (exact integers), over
+    ``float(Qb*4) * pair_size``. Returns float32 ``[B, H, 1, P]``."""
+    B, H, QW, _ = pv_map.shape
+    ex = pv_map[..., :patch_blocks]
+    if patch_blocks % 2:
+        ex = torch.nn.functional.pad(ex, (0, 1))
+    P = (patch_blocks + 1) // 2
+    counts = ex.reshape(B, H, QW, P, 2).sum(dim=(2, 4), dtype=torch.int64)
+    pair_size = torch.full((P,), 2.0, device=pv_map.device, dtype=torch.float32)
+    if patch_blocks % 2:
+        pair_size[-1] = 1.0
+    denom = torch.tensor(float(QW), device=pv_map.device, dtype=torch.float32) * pair_size
+    return (counts.to(torch.float32) / denom).view(B, H, 1, P)
+
+
+def _record_pv_execution(routing_state: dict | None, pv_map: torch.Tensor | None = None,
+                         patch_blocks: int | None = None) -> None:
     """PV-execution service of the layer just attended (SW:8055-8217 with
     ``_reduce_exact_pv_execution_to_pair``, SW:2983-3028).
 
-    The PV threshold is inert (1e10; finite thresholds are rejected by
-    ``routing_config``), so every listed block runs its PV product in each of
-    the four 32-row query waves of its 128-row block: the execution map is
-    the selected support repeated over the waves. The exact reduction,
-    ``(4 * count) / (4 * Q * pair_size)``, divides the same integers as the
-    QK-admission fraction ``count / (Q * pair_size)`` written by the select
-    kernel, so the two are the same float32 values.
+    With the PV post-cut (``pv_map`` given) the service is reduced from the
+    kernel's execution map. At the inert threshold (1e10) every listed block
+    runs its PV product in each of the four 32-row query waves of its 128-row
+    block: the exact reduction ``(4 * count) / (4 * Q * pair_size)`` then
+    divides the same integers as the QK-admission fraction
+    ``count / (Q * pair_size)`` written by the select kernel, so that fraction
+    is recorded as is.
     """
     if routing_state is None:
         return
@@ -207,11 +226,23 @@ def _record_pv_execution(routing_state: dict | None) -> None:
     if pending is None:
         return
     layer_idx, service = pending
+    if pv_map is not None:
+        service = _pv_execution_service(pv_map, patch_blocks)
     routing_state[SERVICE_KEY] = {
         "layer_idx": int(layer_idx),
         "identity_observed": True,
         "pair_service_fraction": service,
     }
+
+
+def _pv_threshold(key: torch.Tensor, layer_idx: int) -> float | None:
+    """The PV post-cut threshold of this layer (SW:7008-7027), or None when
+    it is inert (1e10, or the layer is not in QK_PV_ACTIVE_LAYERS)."""
+    cfg = routing_config()
+    thr = resolve_pv_threshold(cfg.pv_threshold, key.shape[-2])
+    if not pv_threshold_active(cfg.pv_active_layers, layer_idx) or thr >= 1e10:
+        return None
+    return thr
 
 
 def _stats(out: dict, cap: torch.Tensor | None) -> dict:
@@ -420,8 +451,13 @@ def block_sparse_attn_cuda(query: torch.Tensor, key: torch.Tensor, value: torch.
     sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
                                         routing_stats_store, routing_state, num_patch_tokens, research)
     vt = ops.pack_v(value)
-    o = ops.block_sparse_attn(query, key, vt, sel["index"], sel["count"])
-    _record_pv_execution(routing_state)
+    thr = _pv_threshold(key, layer_idx)
+    if thr is None:
+        o = ops.block_sparse_attn(query, key, vt, sel["index"], sel["count"])
+        _record_pv_execution(routing_state)
+    else:
+        o, pv_map = ops.block_sparse_attn_pv(query, key, vt, sel["index"], sel["count"], thr)
+        _record_pv_execution(routing_state, pv_map, pooled_score.shape[-1])
     if o.dtype != query.dtype:
         o = o.to(query.dtype)
     if return_sparsity:
@@ -443,6 +479,12 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
     sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
                                         routing_stats_store, routing_state, num_patch_tokens, research)
     vt = ops.pack_v(value)
-    o_patch, o_special = ops.global_attn(q_patch, q_special, key, vt, sel["index"], sel["count"])
-    _record_pv_execution(routing_state)
+    thr = _pv_threshold(key, layer_idx)
+    if thr is None:
+        o_patch, o_special = ops.global_attn(q_patch, q_special, key, vt, sel["index"], sel["count"])
+        _record_pv_execution(routing_state)
+    else:  # the post-cut applies to the patch queries; the special queries stay dense
+        o_patch, pv_map = ops.block_sparse_attn_pv(q_patch, key, vt, sel["index"], sel["count"], thr)
+        o_special = None if q_special is None else ops.dense_attn(q_special, key, vt)
+        _record_pv_execution(routing_state, pv_map, pooled_score.shape[-1])
     return o_patch, o_special, _sparsity(sel, total_kblk)
