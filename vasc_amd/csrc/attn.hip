@@ -318,20 +318,28 @@ void bsattn_fwd_kernel(const AttnParams p) {
             const int kk = 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
             mx = kk < lim ? fmaxf(mx, S[t][r]) : mx;
           }
-        mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
-        const float gap = wave_max(mx - run_max);
+        mx = fmaxf(mx, xor_lane(mx, 32)) * c;
+        float gap = mx - run_max;  // the wave's largest, by VALU cross-lane moves (rows 0-31, both halves)
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) gap = fmaxf(gap, xor_lane(gap, off));
         run_max = fmaxf(run_max, mx);
         if (l == 0) pv_gap[w] = gap;
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const float g4 = fmaxf(fmaxf(pv_gap[0], pv_gap[1]), fmaxf(pv_gap[2], pv_gap[3]));
-        if (!(g4 + pv_threshold > 0.f)) continue;  // skipped: no P, no sum, no PV
-        if (l == 0 && p.pv_map && cur >= 0 && cur < nkb32)
-          p.pv_map[((bh * p.nqb + qb) * 4 + w) * p.pv_w + cur] = 1;
       }
     }
 
     u32x4 pb[4];
-    float bs = exp_block(S, pb);
+    float bs = exp_block(S, pb);  // changes no state: a skipped block drops it
+    if constexpr (kPv) {
+      if (!dense) {
+        // the workgroup's decision, read after the exponentials so that the
+        // barrier wait overlaps them
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const float g4 = fmaxf(fmaxf(pv_gap[0], pv_gap[1]), fmaxf(pv_gap[2], pv_gap[3]));
+        if (!(g4 + pv_threshold > 0.f)) continue;  // skipped: no sum, no PV
+        if (l == 0 && p.pv_map && cur >= 0 && cur < nkb32)
+          p.pv_map[((bh * p.nqb + qb) * 4 + w) * p.pv_w + cur] = 1;
+      }
+    }
     const int lim = valid_keys(cur);
     if (__ballot(!(bs <= kHigh) || !(ls + bs >= kLow)) || lim < kBlockK) bs = slow(S, pb, lim);
     ls += bs;
