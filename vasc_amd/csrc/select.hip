@@ -476,7 +476,11 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
   const int tid = threadIdx.x;
   if (tid < 64) {
     double acc = 0.0, dacc = 0.0, useful = 0.0, wasted = 0.0, consumed = 0.0;
+    // unrolled so several iterations' loads are in flight; the float64 chains
+    // keep their order
+#pragma unroll 4
     for (int64_t q = tid; q < p.Q; q += 64) acc = acc + static_cast<double>(p.rowpair[bh * p.Q + q]);
+#pragma unroll 4
     for (int64_t pp = tid; pp < p.P; pp += 64) {
       float refl, sig;
       const float d = settle_one(p, bh * p.P + pp, &refl, &sig);
