@@ -193,7 +193,8 @@ __device__ __forceinline__ float settle_one(const SelectParams &p, int64_t i, fl
 __device__ __forceinline__ int service_gate(const SelectParams &p) {
   if (!p.pending) return 0;
   double u = 0.0, w = 0.0, c = 0.0;
-  for (int64_t h = 0; h < p.BH; ++h) {
+#pragma unroll 4
+  for (int64_t h = 0; h < p.BH; ++h) {  // sequential over heads; unrolled for loads in flight
     u = u + p.gate_part[3 * h + 0];
     w = w + p.gate_part[3 * h + 1];
     c = c + p.gate_part[3 * h + 2];
