@@ -69,6 +69,18 @@ int vasc_pool_qkv(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                   float *innovation, void *stream);
 
 /*
+ * predict_attention's pooling with pool_mode="max" (attention.py:31-104,
+ * F.max_pool1d with ceil_mode): per-feature max of Q over 128-token blocks and
+ * of K over 64-token blocks, bf16 (exact). Same layout rules as
+ * vasc_pool_qkv; V and the innovation stay on the mean path.
+ */
+int vasc_pool_qk_max(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                     const uint16_t *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                     int64_t B, int64_t H, int64_t nq, int64_t nk, int64_t d,
+                     int64_t block_q, int64_t block_k, uint16_t *pooled_q,
+                     uint16_t *pooled_k, void *stream);
+
+/*
  * Kernel 1b: pooled attention probabilities
  *   prob = softmax_k( bf16( bf16(pooled_q . pooled_k) * scale ) )  (fp32)
  * i.e. the score/softmax of predict_attention (attention.py:97-101) with the

@@ -57,6 +57,19 @@ def pool_blocks(x: np.ndarray, block: int, *, round_bf16: bool = False) -> np.nd
     return out.astype(np.float32)
 
 
+def max_pool_blocks(x: np.ndarray, block: int) -> np.ndarray:
+    """``F.max_pool1d(kernel_size=block, ceil_mode=True)`` over the tokens of
+    ``x [..., T, D]``: the tail block takes the max of its real tokens (the
+    max of bf16 values is itself a bf16 value, so no rounding)."""
+    x = np.asarray(x, dtype=np.float32)
+    T = x.shape[-2]
+    nb = math.ceil(T / block)
+    out = np.empty(x.shape[:-2] + (nb, x.shape[-1]), dtype=np.float32)
+    for i in range(nb):
+        out[..., i, :] = x[..., i * block:min((i + 1) * block, T), :].max(axis=-2)
+    return out
+
+
 def pooled_logits(pooled_q: np.ndarray, pooled_k: np.ndarray, *, bf16: bool = True) -> np.ndarray:
     """Scaled pooled logits ``[..., Qb, Kb]`` in float32."""
     d = pooled_q.shape[-1]
@@ -76,11 +89,15 @@ def softmax(logits: np.ndarray) -> np.ndarray:
     return (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
 
 
-def pooled_prob(q: np.ndarray, k: np.ndarray, ks_q: int = 128, ks_k: int = 64, *, bf16: bool = True):
-    """``predict_attention(q, k, ks_q, ks_k, pool_mode="avg")`` (ATT:31-104).
+def pooled_prob(q: np.ndarray, k: np.ndarray, ks_q: int = 128, ks_k: int = 64, *, bf16: bool = True,
+                pool_mode: str = "avg"):
+    """``predict_attention(q, k, ks_q, ks_k, pool_mode)`` (ATT:31-104).
 
     Returns ``(prob [B,H,Qb,Kb] float32, pooled_q, pooled_k)``.
     """
-    pq = pool_blocks(q, ks_q, round_bf16=bf16)
-    pk = pool_blocks(k, ks_k, round_bf16=bf16)
+    if pool_mode == "max":
+        pq, pk = max_pool_blocks(q, ks_q), max_pool_blocks(k, ks_k)
+    else:
+        pq = pool_blocks(q, ks_q, round_bf16=bf16)
+        pk = pool_blocks(k, ks_k, round_bf16=bf16)
     return softmax(pooled_logits(pq, pk, bf16=bf16)), pq, pk

@@ -88,6 +88,17 @@ def test_predict_attention_matches_oracle():
     assert np.isclose(p, ref, rtol=1e-4, atol=1e-9).mean() > 0.999
 
 
+def test_predict_attention_max_pooling_matches_oracle():
+    from vasc_amd.attention import predict_attention
+    g = torch.Generator().manual_seed(2)
+    q = (torch.randn(1, 3, 1000, 64, generator=g) * 2).to(torch.bfloat16)
+    k = (torch.randn(1, 3, 1041, 64, generator=g) * 2).to(torch.bfloat16)
+    p = predict_attention(q.cuda(), k.cuda(), pool_mode="max").cpu().numpy()
+    ref, _, _ = OP.pooled_prob(q.float().numpy(), k.float().numpy(), bf16=True, pool_mode="max")
+    assert p.shape == ref.shape
+    assert np.isclose(p, ref, rtol=1e-4, atol=1e-9).mean() > 0.999
+
+
 def test_get_block_mask_bit_exact():
     from vasc_amd.sparse_wrapper import get_block_mask
     rng = np.random.default_rng(2)

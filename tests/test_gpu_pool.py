@@ -141,3 +141,15 @@ def test_pooled_softmax_scale(scale):
         close = np.isclose(got, ref, rtol=2e-5, atol=1e-9)
         need = 1.0 if not rnd else 0.999
         assert close.mean() >= need, f"round={rnd}: {(~close).sum()} of {close.size} differ"
+
+
+@pytest.mark.parametrize("nq,nk", [(1000, 1041), (128, 64), (77, 130), (8288, 8328)])
+def test_pool_qk_max_bit_exact(nq, nk):
+    """Block maxima are exact: bit-identical to the oracle, also for negative
+    values and the ragged tail blocks (missing tokens never win)."""
+    from vasc_amd import ops
+    q, k = (_rand((2, 3, n, 64), s) - 2.0 for n, s in ((nq, 5), (nk, 6)))
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    pq, pk = ops.pool_qk_max(q.cuda(), k.cuda().transpose(1, 2).contiguous().transpose(1, 2))
+    assert np.array_equal(pq.float().cpu().numpy(), OP.max_pool_blocks(q.float().numpy(), 128))
+    assert np.array_equal(pk.float().cpu().numpy(), OP.max_pool_blocks(k.float().numpy(), 64))

@@ -98,7 +98,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES), "ctypes table out of sync with include/vasc_hip.h"
-    assert lib.vasc_abi_version() == 4
+    assert lib.vasc_abi_version() == 5
 
 
 def test_host_only_queries_and_argument_errors():

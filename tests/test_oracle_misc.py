@@ -176,3 +176,15 @@ def test_pv_post_cut_boundary_inert_and_padded_rows():
     assert OA.pv_post_cut(q, k, idx, c1, 1.0)[1][0, 0, 0] == 2           # padded rows: 0 and 0, gap 0
     q, k = _rank_one([-50 / u, -60 / u], Nq=128, a=1.0)
     assert OA.pv_post_cut(q, k, idx, c1, 1.0)[1][0, 0, 0] == 1           # no padding: gap -10
+
+
+def test_max_pool_blocks_matches_torch():
+    """``max_pool_blocks`` is F.max_pool1d(kernel, ceil_mode=True) on bf16 data,
+    including ragged tails and all-negative blocks."""
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(3)
+    for T, blk in ((1000, 128), (1041, 64), (64, 64), (7, 64)):
+        x = (torch.randn(2, 3, T, 64, generator=g) - 3.0).to(torch.bfloat16).float()
+        ref = F.max_pool1d(x.reshape(6, T, 64).transpose(1, 2), blk, ceil_mode=True).transpose(1, 2)
+        got = OP.max_pool_blocks(x.numpy(), blk)
+        assert np.array_equal(got, ref.reshape(2, 3, -1, 64).numpy())

@@ -25,6 +25,8 @@ I32 = c_int32
 SIGNATURES: dict[str, tuple] = {
     "vasc_last_error": (ctypes.c_char_p, []),
     "vasc_abi_version": (c_int32, []),
+    "vasc_pool_qk_max": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64, I64, I64, I64,
+                                  P, P, P]),
     "vasc_pool_qkv": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64,
                                 I64, I64, I64, I64, I64, I64, I64, P, P, P, P, P]),
     "vasc_pooled_softmax": (c_int32, [P, P, I64, I64, I64, I64, I64, c_float, I32, P, P, P]),

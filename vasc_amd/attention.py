@@ -24,18 +24,20 @@ def predict_attention(query: torch.Tensor, key: torch.Tensor, ks_q: int = 128, k
                       pool_mode: str = "avg", return_key_block_variance: bool = False) -> torch.Tensor:
     """Pooled attention probabilities ``[B,H,ceil(Tq/ks_q),ceil(Tk/ks_k)]`` (fp32).
 
-    Pooled means are rounded to bf16 and the logits follow the bf16 matmul
-    of the reference's autocast run; the softmax is fp32.
+    Pooled means are rounded to bf16 (block maxima are exact) and the logits
+    follow the bf16 matmul of the reference's autocast run; the softmax is
+    fp32.
     """
     assert pool_mode in ("max", "avg"), f"{pool_mode=}"
     assert query.ndim == 4 and key.ndim == 4
-    if pool_mode != "avg":
-        raise NotImplementedError("max pooling is not built (the release modes pool with avg)")
     if (ks_q, ks_k) != (ops.BLOCK_Q, ops.BLOCK_K):
         raise NotImplementedError("pooling is built for 128-token query and 64-token key blocks")
     if return_key_block_variance:
         raise NotImplementedError("key block variance feeds a research router that is not built")
-    pq, pk, _, _ = ops.pool_qkv(q=query, k=key, innovation=False)
+    if pool_mode == "max":
+        pq, pk = ops.pool_qk_max(query, key)
+    else:
+        pq, pk, _, _ = ops.pool_qkv(q=query, k=key, innovation=False)
     return ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(query.shape[-1]))
 
 

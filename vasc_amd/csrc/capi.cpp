@@ -27,4 +27,4 @@ int check_launch(const char *what) {
 
 extern "C" const char *vasc_last_error(void) { return vasc::g_error; }
 
-extern "C" int vasc_abi_version(void) { return 4; }
+extern "C" int vasc_abi_version(void) { return 5; }

@@ -81,6 +81,12 @@ constexpr int kQuadXor1 = 0xb1;   // quad_perm [1, 0, 3, 2]
 constexpr int kQuadXor2 = 0x4e;   // quad_perm [2, 3, 0, 1]
 constexpr int kHalfMirror = 0x141;
 
+__device__ __forceinline__ float group8_max(float v) {
+  v = fmaxf(v, dpp<kQuadXor1>(v));
+  v = fmaxf(v, dpp<kQuadXor2>(v));
+  return fmaxf(v, dpp<kHalfMirror>(v));
+}
+
 __device__ __forceinline__ float group8_sum(float v) {
   v += dpp<kQuadXor1>(v);
   v += dpp<kQuadXor2>(v);

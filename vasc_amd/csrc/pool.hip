@@ -39,6 +39,10 @@ struct PoolParams {
   int64_t H, npairs;
 };
 
+// kMax: block max of Q and K instead of the mean (predict_attention with
+// pool_mode="max", F.max_pool1d with ceil_mode: a tail block takes the max of
+// its real tokens). The max of bf16 values is exact; V is not pooled here.
+template <bool kMax>
 __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
   __shared__ float red[3][2][4][kHeadDim];
   __shared__ float pv[2][kHeadDim];
@@ -60,8 +64,9 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int64_t tok = chunk * 128 + 32 * u + 8 * w + t8;
+      constexpr uint32_t kPad = kMax ? 0xff80ff80u : 0u;  // -inf pairs: missing tokens never win a max
       raw[X][u] = (src && tok < p.ntok[X]) ? *reinterpret_cast<const u32x4 *>(src + tok * p.st[X])
-                                           : u32x4{0, 0, 0, 0};
+                                           : u32x4{kPad, kPad, kPad, kPad};
     }
   }
 #pragma unroll
@@ -71,19 +76,25 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
 #pragma unroll
     for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[half][i] = 0.f;
+      for (int i = 0; i < 8; ++i) acc[half][i] = kMax ? -INFINITY : 0.f;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        acc[u >> 1][2 * i] += __uint_as_float(raw[X][u][i] << 16);
-        acc[u >> 1][2 * i + 1] += __uint_as_float(raw[X][u][i] & 0xffff0000u);
+        const float lo = __uint_as_float(raw[X][u][i] << 16), hi = __uint_as_float(raw[X][u][i] & 0xffff0000u);
+        if (kMax) {
+          acc[u >> 1][2 * i] = fmaxf(acc[u >> 1][2 * i], lo);
+          acc[u >> 1][2 * i + 1] = fmaxf(acc[u >> 1][2 * i + 1], hi);
+        } else {
+          acc[u >> 1][2 * i] += lo;
+          acc[u >> 1][2 * i + 1] += hi;
+        }
       }
     }
 #pragma unroll
     for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[half][i] = group8_sum(acc[half][i]);
+      for (int i = 0; i < 8; ++i) acc[half][i] = kMax ? group8_max(acc[half][i]) : group8_sum(acc[half][i]);
     if (t8 == 0) {
 #pragma unroll
       for (int half = 0; half < 2; ++half)
@@ -102,20 +113,27 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(const PoolParams p) {
     float sum;
     int64_t blk, count;
     if (X == 0) {
-      sum = ((red[0][0][0][d] + red[0][0][1][d]) + (red[0][0][2][d] + red[0][0][3][d])) +
-            ((red[0][1][0][d] + red[0][1][1][d]) + (red[0][1][2][d] + red[0][1][3][d]));
+      if (kMax)
+        sum = fmaxf(fmaxf(fmaxf(red[0][0][0][d], red[0][0][1][d]), fmaxf(red[0][0][2][d], red[0][0][3][d])),
+                    fmaxf(fmaxf(red[0][1][0][d], red[0][1][1][d]), fmaxf(red[0][1][2][d], red[0][1][3][d])));
+      else
+        sum = ((red[0][0][0][d] + red[0][0][1][d]) + (red[0][0][2][d] + red[0][0][3][d])) +
+              ((red[0][1][0][d] + red[0][1][1][d]) + (red[0][1][2][d] + red[0][1][3][d]));
       blk = chunk;
       count = p.ntok[0] - chunk * 128;
       count = count > 128 ? 128 : count;
     } else {
       const int half = (slot - 1) & 1;
-      sum = (red[X][half][0][d] + red[X][half][1][d]) + (red[X][half][2][d] + red[X][half][3][d]);
+      if (kMax)
+        sum = fmaxf(fmaxf(red[X][half][0][d], red[X][half][1][d]), fmaxf(red[X][half][2][d], red[X][half][3][d]));
+      else
+        sum = (red[X][half][0][d] + red[X][half][1][d]) + (red[X][half][2][d] + red[X][half][3][d]);
       blk = 2 * chunk + half;
       count = p.ntok[X] - blk * 64;
       count = count > 64 ? 64 : count;
     }
     if (count <= 0) continue;
-    const uint16_t mean = f32_to_bf16(sum / static_cast<float>(count));
+    const uint16_t mean = f32_to_bf16(kMax ? sum : sum / static_cast<float>(count));  // a max is exact in bf16
     p.out[X][(bh * p.nblk[X] + blk) * kHeadDim + d] = mean;
     if (X == 2) pv[slot - 3][d] = bf16_to_f32(mean);
   }
@@ -401,12 +419,13 @@ __global__ __launch_bounds__(kBlockWaves * 64) void pooled_prob_kernel(const Blo
 }  // namespace
 }  // namespace vasc
 
-extern "C" int vasc_pool_qkv(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st, const uint16_t *k,
+namespace vasc {
+namespace {
+int pool_impl(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st, const uint16_t *k,
                              int64_t k_sb, int64_t k_sh, int64_t k_st, const uint16_t *v, int64_t v_sb,
                              int64_t v_sh, int64_t v_st, int64_t B, int64_t H, int64_t nq, int64_t nk, int64_t d,
                              int64_t block_q, int64_t block_k, uint16_t *pooled_q, uint16_t *pooled_k,
-                             uint16_t *pooled_v, float *innovation, void *stream) {
-  using namespace vasc;
+                             uint16_t *pooled_v, float *innovation, void *stream, bool pool_max) {
   VASC_SUPPORTED(d == 64 && block_q == 128 && block_k == 64,
                  "pooling variant d=%lld block_q=%lld block_k=%lld not built (built: 64/128/64)", (long long)d,
                  (long long)block_q, (long long)block_k);
@@ -445,8 +464,32 @@ extern "C" int vasc_pool_qkv(const uint16_t *q, int64_t q_sb, int64_t q_sh, int6
   p.npairs = cdiv(p.nblk[2], 2);
   const int64_t chunks = cdiv(q ? nq : 0, 128) > cdiv(nk, 128) ? cdiv(nq, 128) : cdiv(nk, 128);
   VASC_REQUIRE(chunks < (int64_t(1) << 31) && B * H < 65536, "grid too large");
-  hipLaunchKernelGGL(pool_qkv_kernel, dim3(chunks, B * H), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), p);
-  return check_launch("vasc_pool_qkv");
+  if (pool_max)
+    hipLaunchKernelGGL(pool_qkv_kernel<true>, dim3(chunks, B * H), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       p);
+  else
+    hipLaunchKernelGGL(pool_qkv_kernel<false>, dim3(chunks, B * H), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), p);
+  return check_launch(pool_max ? "vasc_pool_qk_max" : "vasc_pool_qkv");
+}
+}  // namespace
+}  // namespace vasc
+
+extern "C" int vasc_pool_qkv(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st, const uint16_t *k,
+                             int64_t k_sb, int64_t k_sh, int64_t k_st, const uint16_t *v, int64_t v_sb,
+                             int64_t v_sh, int64_t v_st, int64_t B, int64_t H, int64_t nq, int64_t nk, int64_t d,
+                             int64_t block_q, int64_t block_k, uint16_t *pooled_q, uint16_t *pooled_k,
+                             uint16_t *pooled_v, float *innovation, void *stream) {
+  return vasc::pool_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, B, H, nq, nk, d, block_q,
+                         block_k, pooled_q, pooled_k, pooled_v, innovation, stream, false);
+}
+
+extern "C" int vasc_pool_qk_max(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st, const uint16_t *k,
+                                int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t B, int64_t H, int64_t nq,
+                                int64_t nk, int64_t d, int64_t block_q, int64_t block_k, uint16_t *pooled_q,
+                                uint16_t *pooled_k, void *stream) {
+  return vasc::pool_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, nullptr, 0, 0, 8, B, H, nq, nk, d, block_q,
+                         block_k, pooled_q, pooled_k, nullptr, nullptr, stream, true);
 }
 
 extern "C" int vasc_pair_innovation(const float *pooled_v, int64_t B, int64_t H, int64_t kb, int64_t d,

@@ -44,6 +44,20 @@ def _ptr(t):
 
 
 # ----------------------------------------------------------------- kernel 1
+def pool_qk_max(q: torch.Tensor, k: torch.Tensor):
+    """Block max pooling of Q (128 tokens) and K (64 tokens), bf16:
+    ``predict_attention(pool_mode="max")``'s pooling."""
+    q = _bhtd(q, "q")
+    k = _bhtd(k, "k")
+    B, H, nq, D = q.shape
+    nk = k.shape[2]
+    pq = torch.empty(B, H, math.ceil(nq / BLOCK_Q), D, device=q.device, dtype=torch.bfloat16)
+    pk = torch.empty(B, H, math.ceil(nk / BLOCK_K), D, device=q.device, dtype=torch.bfloat16)
+    _lib.call("vasc_pool_qk_max", q.data_ptr(), *q.stride()[:3], k.data_ptr(), *k.stride()[:3], B, H, nq, nk, D,
+              BLOCK_Q, BLOCK_K, pq.data_ptr(), pk.data_ptr(), _stream())
+    return pq, pk
+
+
 def pool_qkv(q=None, k=None, v=None, *, innovation: bool = True):
     """Block mean pooling (bf16-rounded) of Q (128) and K, V (64) + V pair innovation.
 
