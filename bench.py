@@ -54,7 +54,7 @@ def log(msg: str) -> None:
 
 def synthetic_layer(N: int, P: int, S: int, H: int, D: int, seed: int, device):
     """Q (patch only), K, V in [patch; special] order: N(0,1) plus a per-frame
-    rank-8 component of scale 0.5 (the survey's synthetic recipe)."""
+    rank-8 component of scale 0.5 (the input recipe of the C1 configuration)."""
     g = torch.Generator(device=device).manual_seed(seed)
     out = []
     for _ in range(3):

@@ -7,7 +7,7 @@ TEST INFRASTRUCTURE (see ``oracle/__init__.py``).
 for each row the selected columns in ascending order, stored as deltas (the
 first entry absolute), zero-filled, plus the count. ``decode`` inverts it.
 
-Pinning: ``tests/test_oracle_lut.py`` checks ``encode`` against an
+Pinning: ``tests/test_oracle_misc.py`` checks ``encode`` against an
 independent restatement of the reference's torch ``block_map_lut``
 (``utils.py:417-430``: cumsum, sort, difference) and checks
 ``decode(encode(m)) == m`` on random maps including empty and full rows.

@@ -14,7 +14,7 @@ TEST INFRASTRUCTURE (see ``oracle/__init__.py``).
                     rounded to bf16 by the bf16 matmul, the scale multiply
                     rounded to bf16, softmax in fp32 (autocast promotes it).
 
-Parity pins: ``tests/test_oracle_pooling.py`` checks the pooling against
+Parity pins: ``tests/test_oracle_misc.py`` checks the pooling against
 brute-force per-block means (exact rational arithmetic on small cases) and
 against ``torch.nn.functional.avg_pool1d(ceil_mode=True)``; the predictor
 against golden vectors from the reference's ``predict_attention`` run on CPU in

@@ -9,11 +9,12 @@ Follows ``evaluate.py:16-32`` of the reference with the constants of
 QK budget is ``int(Kb*(1-s))``, at least 1 (``SW:1226-1228``,
 ``spas_sage_attn/utils.py:289``).
 
-Pinning: ``tests/test_oracle_profile.py`` replays the reference's
+Pinning: ``tests/test_oracle_misc.py`` replays the reference's
 ``tests/test_release.py:43-51, 109-121`` assertions (24/18 values, mean equal
 to ``s`` to 1e-9, favoured layer ``s-0.05``, ``None`` at 0.65 and 0.70,
-active at 0.7001, ValueError when the profile leaves [0,1)) and the survey's
-budget table (C2: 155/120 blocks, C3: 362/224, C4: 310/233).
+active at 0.7001, ValueError when the profile leaves [0,1)) and the per-layer
+budgets of the benchmark configurations worked out by hand (C2: 155/120
+blocks, C3: 362/224, C4: 310/233).
 """
 from __future__ import annotations
 

@@ -100,7 +100,7 @@ def test_structural_profile_matches_release_assertions():
             PR.layer_sparsity(model, .99)
 
 
-def test_budget_table_of_the_survey():
+def test_budget_table_of_the_configs():
     c2 = PR.layer_sparsity("vggt", .75)
     assert {PR.budget(518, s) for s in c2} == {155, 120}
     c3 = PR.layer_sparsity("vggt", .875)
