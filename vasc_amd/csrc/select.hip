@@ -475,6 +475,18 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
   __shared__ float sh_pc, sh_dsum;
   const int64_t bh = blockIdx.y;
   const int tid = threadIdx.x;
+  // this thread's pair: its chunk partials and ledger inputs do not depend on
+  // the per-head sums below, so they load before the barrier
+  const int64_t pp = static_cast<int64_t>(blockIdx.x) * 256 + tid;
+  const bool has = pp < p.P;
+  double acc_pp = 0.0;
+  float refl_pp = 0.f, sig_pp = 0.f, d_pp = 0.f;
+  if (has) {
+    const double *part = p.part + bh * p.nchunks * p.P + pp;
+#pragma unroll 8
+    for (int64_t c = 0; c < p.nchunks; ++c) acc_pp = acc_pp + part[c * p.P];
+    d_pp = settle_one(p, bh * p.P + pp, &refl_pp, &sig_pp);
+  }
   if (tid < 64) {
     double acc = 0.0, dacc = 0.0, useful = 0.0, wasted = 0.0, consumed = 0.0;
     // unrolled so several iterations' loads are in flight; the float64 chains
@@ -506,16 +518,10 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
     }
   }
   __syncthreads();
-  const int64_t pp = static_cast<int64_t>(blockIdx.x) * 256 + tid;
-  if (pp >= p.P) return;
-  double acc = 0.0;
-  const double *part = p.part + bh * p.nchunks * p.P + pp;
-#pragma unroll 8
-  for (int64_t c = 0; c < p.nchunks; ++c) acc = acc + part[c * p.P];
-  p.arrival_out[bh * p.P + pp] = static_cast<float>(acc / static_cast<double>(p.Q));
+  if (!has) return;
+  p.arrival_out[bh * p.P + pp] = static_cast<float>(acc_pp / static_cast<double>(p.Q));
   p.counts[bh * p.P + pp] = 0;
-  float refl, sig;
-  const float d = settle_one(p, bh * p.P + pp, &refl, &sig);
+  const float d = d_pp;
   p.debt_out[bh * p.P + pp] = d;
   const float dsum = sh_dsum;
   const float scale = sh_pc / floor_tiny(dsum);
