@@ -142,7 +142,11 @@ size_t vasc_select_workspace_size(int64_t B, int64_t H, int64_t q_blocks,
  * sink_blocks trailing always-on blocks K..K+sink-1 appended to each list.
  * debt_in, pending_arrival, prev_service [B,H,P] float32, each may be NULL
  *             (NULL pending = no previous layer to settle).
- * debt_out, arrival_out, service_out [B,H,P] float32 (VASC, required).
+ * debt_out, arrival_out, service_out [B,H,P] float32 (VASC, required),
+ *             each disjoint from the three inputs and from each other: the
+ *             ledger cannot be updated in place (one head's inputs are read
+ *             by every workgroup of the head while others write its
+ *             outputs). Overlapping ranges are rejected (VASC_ERR_ARGUMENT).
  * gate_out    optional int32 scalar: 1 when the debt priority was used.
  * priority_out optional [B,H,Q,K] float32 execution priority.
  * mask_out    optional [B,H,Q,K] uint8 support of the patch blocks.

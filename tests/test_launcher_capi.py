@@ -153,3 +153,31 @@ def test_host_only_queries_and_argument_errors():
     rc = lib.vasc_block_sparse_attn_pv_fwd(None, 0, 0, 8, None, 0, 0, 8, None, None, 0, 0, 8, 1, 1, 128, 64, 64,
                                            None, 1, None, 0, ctypes.c_float(0.125), None, None, None)
     assert rc == 1 and b"pv_threshold" in lib.vasc_last_error()
+
+
+def test_select_rejects_ledger_aliasing():
+    """The ledger cannot be updated in place: the VASC head pass reads all of a
+    head's ledger inputs while other workgroups write its outputs. Overlapping
+    output/input ranges are rejected before any launch."""
+    lib = _lib.load()
+    B, H, Q, K = 1, 2, 3, 10
+    P = (K + 1) // 2
+    n = B * H * P * 4  # bytes of one ledger tensor
+    base = 1 << 20
+    fake = lambda off: ctypes.c_void_p(base + off)  # noqa: E731 (never dereferenced)
+    score, inn, idx, cnt, ws = fake(0), fake(4096), fake(8192), fake(12288), fake(16384)
+    d_in, pend, prev = fake(65536), fake(65536 + 4096), fake(65536 + 8192)
+
+    def call(debt_out, arrival_out, service_out):
+        return lib.vasc_select_blocks(score, inn, B, H, Q, K, _lib.MODE_VASC, 3, None, None, 0, 3, 0,
+                                      d_in, pend, prev, debt_out, arrival_out, service_out, None, None, None,
+                                      idx, 3, cnt, ws, 1 << 20, None)
+
+    for outs in ((d_in, fake(20480), fake(24576)),           # debt updated in place
+                 (fake(20480), pend, fake(24576)),           # arrival over pending
+                 (fake(20480), fake(24576), prev),           # service over prev_service
+                 (fake(65536 + 4), fake(20480), fake(24576)),  # partial overlap
+                 (fake(20480), fake(20480 + n - 4), fake(24576))):  # outputs overlapping each other
+        assert call(*outs) == 1
+        assert b"overlap" in lib.vasc_last_error()
+

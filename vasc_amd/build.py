@@ -37,7 +37,7 @@ SOURCES = {
     # the rotary embedding rounds its products and sum separately, as torch does
     "layout.hip": ["-ffp-contract=off"],
     "pool.hip": ["-ffp-contract=off"],
-    "select.hip": ["-ffp-contract=off"],
+    "select.hip": ["-ffp-contract=off", "-Wshadow"],
 }
 
 

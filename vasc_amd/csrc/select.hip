@@ -494,9 +494,9 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
 #pragma unroll 4
     for (int64_t q = tid; q < p.Q; q += 64) acc = acc + static_cast<double>(p.rowpair[bh * p.Q + q]);
 #pragma unroll 4
-    for (int64_t pp = tid; pp < p.P; pp += 64) {
+    for (int64_t j = tid; j < p.P; j += 64) {
       float refl, sig;
-      const float d = settle_one(p, bh * p.P + pp, &refl, &sig);
+      const float d = settle_one(p, bh * p.P + j, &refl, &sig);
       dacc = dacc + static_cast<double>(d);
       useful = useful + static_cast<double>(clamp_min0(sig - refl));
       wasted = wasted + static_cast<double>(refl);
@@ -1197,11 +1197,11 @@ Workspace layout(int64_t B, int64_t H, int64_t Q, int64_t K) {
   return w;
 }
 
-int reserve_lds(const void *kern, size_t lds) {
-  if (lds <= 64 * 1024) return VASC_OK;
-  const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+int reserve_lds(const void *kern, size_t lds_bytes) {
+  if (lds_bytes <= 64 * 1024) return VASC_OK;
+  const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes));
   if (e != hipSuccess) {
-    set_error("vasc_select_blocks: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(e));
+    set_error("vasc_select_blocks: cannot reserve %zu bytes of LDS: %s", lds_bytes, hipGetErrorString(e));
     return VASC_ERR_HIP;
   }
   return VASC_OK;
@@ -1214,13 +1214,13 @@ int launch_select_cfg(const SelectParams &p, hipStream_t s) {
   // keep the global count atomics down.
   const int64_t rows = p.BH * p.Q;
   const int rpw = static_cast<int>(rows >= 4 * 8192 ? 4 : (rows >= 2 * 8192 ? 2 : 1));
-  const size_t lds =
+  const size_t lds_bytes =
       (static_cast<size_t>(kWaves) * wave_lds_words<EPT>() + (kVasc ? static_cast<size_t>(p.P + 1) / 2 + 64 : 0)) * 4;
   const void *kern = reinterpret_cast<const void *>(select_kernel<kVasc, EPT>);
   int rc;
-  if ((rc = reserve_lds(kern, lds))) return rc;
+  if ((rc = reserve_lds(kern, lds_bytes))) return rc;
   const dim3 grid(static_cast<unsigned>(cdiv(p.Q, static_cast<int64_t>(kWaves) * rpw)), static_cast<unsigned>(p.BH));
-  hipLaunchKernelGGL((select_kernel<kVasc, EPT>), grid, dim3(256), lds, s, p, rpw);
+  hipLaunchKernelGGL((select_kernel<kVasc, EPT>), grid, dim3(256), lds_bytes, s, p, rpw);
   return check_launch("vasc_select_blocks/select");
 }
 
@@ -1252,12 +1252,12 @@ int launch_select(const SelectParams &p, bool vasc, hipStream_t s) {
 template <int EPT>
 int launch_arrival_reg_cfg(const SelectParams &p, hipStream_t s) {
   constexpr int kRowWaves = EPT <= 16 ? 16 : (EPT <= 36 ? 8 : 4);
-  const size_t lds = static_cast<size_t>((1 + kRowWaves) * p.P) * 4;  // innovation + pair arrivals per row wave
+  const size_t lds_bytes = static_cast<size_t>((1 + kRowWaves) * p.P) * 4;  // innovation + pair arrivals per row wave
   const void *kern = reinterpret_cast<const void *>(arrival_reg_kernel<EPT, kRowWaves>);
   int rc;
-  if ((rc = reserve_lds(kern, lds))) return rc;
+  if ((rc = reserve_lds(kern, lds_bytes))) return rc;
   hipLaunchKernelGGL((arrival_reg_kernel<EPT, kRowWaves>),
-                     dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)), dim3(64 * kRowWaves), lds,
+                     dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)), dim3(64 * kRowWaves), lds_bytes,
                      s, p);
   return VASC_OK;
 }
@@ -1283,10 +1283,10 @@ int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
       // 64 KB; the column partials then need P <= 16 * (64 * waves).
       int aw = 16;
       while (aw > 4 && static_cast<size_t>(aw) * bufn * 4 > 64 * 1024) aw >>= 1;
-      const size_t lds = static_cast<size_t>(aw) * bufn * 4;
-      if ((rc = reserve_lds(reinterpret_cast<const void *>(arrival_kernel), lds))) return rc;
+      const size_t lds_bytes = static_cast<size_t>(aw) * bufn * 4;
+      if ((rc = reserve_lds(reinterpret_cast<const void *>(arrival_kernel), lds_bytes))) return rc;
       hipLaunchKernelGGL(arrival_kernel, dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)),
-                         dim3(64 * aw), lds, s, p, static_cast<int>(bufn));
+                         dim3(64 * aw), lds_bytes, s, p, static_cast<int>(bufn));
     }
     if ((rc = check_launch("vasc_select_blocks/arrival"))) return rc;
     hipLaunchKernelGGL(head_kernel, dim3(static_cast<unsigned>(cdiv(p.P, 256)), static_cast<unsigned>(p.BH)),
@@ -1309,15 +1309,23 @@ extern "C" size_t vasc_select_workspace_size(int64_t B, int64_t H, int64_t q_blo
   return vasc::layout(B, H, q_blocks, k_blocks).bytes;
 }
 
-extern "C" int vasc_select_blocks(const float *score, const float *innovation, int64_t B, int64_t H, int64_t Q,
-                                  int64_t K, int32_t mode, int32_t topk, const int32_t *row_cap,
-                                  const uint8_t *protected_mask, int32_t force_last, int32_t max_capacity,
-                                  int32_t sink_blocks, const float *debt_in, const float *pending_arrival,
-                                  const float *prev_service, float *debt_out, float *arrival_out,
-                                  float *service_out, int32_t *gate_out, float *priority_out, uint8_t *mask_out,
-                                  int32_t *index_out, int64_t width, int32_t *count_out, void *workspace,
-                                  size_t workspace_bytes, void *stream) {
-  using namespace vasc;
+namespace vasc {
+namespace {
+
+// Byte ranges [a, a + n) and [b, b + n) overlap (NULL never overlaps).
+bool overlaps(const void *a, const void *b, size_t n) {
+  if (!a || !b) return false;
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + n && y < x + n;
+}
+
+int select_blocks_impl(const float *score, const float *innovation, int64_t B, int64_t H, int64_t Q, int64_t K,
+                       int32_t mode, int32_t topk, const int32_t *row_cap, const uint8_t *protected_mask,
+                       int32_t force_last, int32_t max_capacity, int32_t sink_blocks, const float *debt_in,
+                       const float *pending_arrival, const float *prev_service, float *debt_out,
+                       float *arrival_out, float *service_out, int32_t *gate_out, float *priority_out,
+                       uint8_t *mask_out, int32_t *index_out, int64_t width, int32_t *count_out, void *workspace,
+                       size_t workspace_bytes, void *stream) {
   VASC_REQUIRE(score && index_out && count_out, "score, index_out and count_out are required");
   VASC_REQUIRE((reinterpret_cast<uintptr_t>(score) & 15) == 0, "score must be 16-byte aligned");
   VASC_REQUIRE(B > 0 && H > 0 && Q > 0 && K > 0, "sizes must be positive");
@@ -1332,6 +1340,17 @@ extern "C" int vasc_select_blocks(const float *score, const float *innovation, i
     VASC_REQUIRE(innovation && debt_out && arrival_out && service_out, "VASC needs innovation and state outputs");
     VASC_REQUIRE(max_capacity >= 0, "max_capacity must be non-negative");
     VASC_REQUIRE(!prev_service || pending_arrival, "prev_service without pending_arrival");
+    // The head pass reads every ledger input of a head while other
+    // workgroups write that head's outputs: in-place updates would race.
+    const size_t ledger = static_cast<size_t>(B * H * ((K + 1) / 2)) * sizeof(float);
+    const float *ins[3] = {debt_in, pending_arrival, prev_service};
+    const float *outs[3] = {debt_out, arrival_out, service_out};
+    for (const float *o : outs)
+      for (const float *i : ins)
+        VASC_REQUIRE(!overlaps(o, i, ledger), "ledger outputs must not overlap the ledger inputs");
+    VASC_REQUIRE(!overlaps(debt_out, arrival_out, ledger) && !overlaps(debt_out, service_out, ledger) &&
+                     !overlaps(arrival_out, service_out, ledger),
+                 "ledger outputs must not overlap each other");
     maxc = max_capacity < K ? max_capacity : K;
   } else {
     // row_cap: per-row counts, each at most max_capacity (K when 0)
@@ -1384,6 +1403,23 @@ extern "C" int vasc_select_blocks(const float *score, const float *innovation, i
   p.counts = vasc ? reinterpret_cast<int32_t *>(wsb + ws.counts) : nullptr;
 
   return launch_rows(p, vasc, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+}  // namespace vasc
+
+extern "C" int vasc_select_blocks(const float *score, const float *innovation, int64_t B, int64_t H, int64_t Q,
+                                  int64_t K, int32_t mode, int32_t topk, const int32_t *row_cap,
+                                  const uint8_t *protected_mask, int32_t force_last, int32_t max_capacity,
+                                  int32_t sink_blocks, const float *debt_in, const float *pending_arrival,
+                                  const float *prev_service, float *debt_out, float *arrival_out,
+                                  float *service_out, int32_t *gate_out, float *priority_out, uint8_t *mask_out,
+                                  int32_t *index_out, int64_t width, int32_t *count_out, void *workspace,
+                                  size_t workspace_bytes, void *stream) {
+  return vasc::select_blocks_impl(score, innovation, B, H, Q, K, mode, topk, row_cap, protected_mask, force_last,
+                                  max_capacity, sink_blocks, debt_in, pending_arrival, prev_service, debt_out,
+                                  arrival_out, service_out, gate_out, priority_out, mask_out, index_out, width,
+                                  count_out, workspace, workspace_bytes, stream);
 }
 
 extern "C" int vasc_settle_terminal(const float *debt_in, const float *pending_arrival, const float *service,
