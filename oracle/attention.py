@@ -27,11 +27,13 @@ import numpy as np
 
 
 def block_sparse_attention(q, k, v, index_lists, counts, *, block_q: int = 128,
-                           block_k: int = 64, scale: float | None = None) -> np.ndarray:
+                           block_k: int = 64, scale: float | None = None, q_blocks=None) -> np.ndarray:
     """float64 attention of ``q [B,H,Nq,D]`` over listed key blocks.
 
     ``index_lists [B,H,Qb,W]`` absolute key-block indices (entries past
     ``counts`` ignored). Rows with a zero count produce zeros.
+    ``q_blocks`` (optional): only these query blocks are computed, the rows
+    of the others stay zero (sampled checks of long sequences).
     """
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
@@ -41,9 +43,10 @@ def block_sparse_attention(q, k, v, index_lists, counts, *, block_q: int = 128,
     scale = D ** -0.5 if scale is None else scale
     Qb = -(-Nq // block_q)
     out = np.zeros((B, H, Nq, v.shape[-1]), np.float64)
+    blocks_to_do = range(Qb) if q_blocks is None else sorted({int(i) for i in q_blocks})
     for b in range(B):
         for h in range(H):
-            for i in range(Qb):
+            for i in blocks_to_do:
                 n = int(counts[b, h, i])
                 if n == 0:
                     continue

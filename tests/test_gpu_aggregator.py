@@ -8,10 +8,16 @@
 * VASC mode: the ledger is cleared at the start of a forward and settled
   after the last layer, so two forwards on the same input are bit-identical
   and the pending arrival is gone afterwards (finalize, sparse_wrapper.py:
-  4101-4177); the per-layer sparsity is recorded when aux_output is on.
+  4101-4177); the per-layer sparsity is recorded when aux_output is on;
+* sparse forwards (VGGT vasc, Pi3 vasc and topk) vs the same float32
+  restatement with each global layer restricted to the index lists the GPU
+  selection produced (teacher-forced; recorded at the selection call), and
+  the recorded lists bit-exact with the oracle selector chain fed the GPU's
+  pooled scores and innovations.
 """
 import os
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -34,7 +40,29 @@ def _model(cls, **kw):
     return m.cuda()
 
 
-def _ref_attention(attn, x, pos):
+def _patch_first(N, P, S, device):
+    """Frame-major token index of each position of the [all patches; all
+    specials] order the sparse layer uses."""
+    f = torch.arange(N, device=device).view(N, 1)
+    patch = (f * P + S + torch.arange(P - S, device=device).view(1, -1)).reshape(-1)
+    special = (f * P + torch.arange(S, device=device).view(1, -1)).reshape(-1)
+    return torch.cat([patch, special])
+
+
+def _list_mask(index, count, n_patch, n_total):
+    """Token mask [B,H,n_patch,n_total] of 128-query x 64-key block lists (patch-first order)."""
+    B, H, Qb, W = index.shape
+    kbt = -(-n_total // 64)
+    live = torch.arange(W, device=index.device).view(1, 1, 1, W) < count.unsqueeze(-1)
+    bm = torch.zeros(B, H, Qb, kbt + 1, dtype=torch.bool, device=index.device)
+    bm.scatter_(3, torch.where(live, index.long(), kbt), True)
+    return bm[..., :kbt].repeat_interleave(128, 2)[:, :, :n_patch].repeat_interleave(64, 3)[..., :n_total]
+
+
+def _ref_attention(attn, x, pos, sparse=None):
+    """float32 attention of one block; ``sparse = (N, P, S, index, count)``
+    restricts the patch queries of a global layer to their listed blocks
+    (special-token queries attend to every key)."""
     B, T, C = x.shape
     H = attn.num_heads
     D = C // H
@@ -43,18 +71,28 @@ def _ref_attention(attn, x, pos):
     q = F.layer_norm(q, (D,), attn.q_norm.weight.float(), attn.q_norm.bias.float(), attn.q_norm.eps)
     k = F.layer_norm(k, (D,), attn.k_norm.weight.float(), attn.k_norm.bias.float(), attn.k_norm.eps)
     q, k = attn.rope(q, pos), attn.rope(k, pos)
-    o = F.scaled_dot_product_attention(q, k, v)
+    if sparse is None:
+        o = F.scaled_dot_product_attention(q, k, v)
+    else:
+        N, P, S, index, count = sparse
+        n_patch = N * (P - S)
+        perm = _patch_first(N, P, S, x.device)
+        mask = torch.ones(B, H, T, T, dtype=torch.bool, device=x.device)
+        mask[:, :, :n_patch] = _list_mask(index, count, n_patch, T)
+        o_re = F.scaled_dot_product_attention(q[:, :, perm], k[:, :, perm], v[:, :, perm], attn_mask=mask)
+        o = torch.empty_like(o_re)
+        o[:, :, perm] = o_re
     return F.linear(o.transpose(1, 2).reshape(B, T, C), attn.proj.weight.float(), attn.proj.bias.float())
 
 
-def _ref_block(blk, x, pos):
+def _ref_block(blk, x, pos, sparse=None):
     ln = lambda m, t: F.layer_norm(t, m.normalized_shape, m.weight.float(), m.bias.float(), m.eps)  # noqa: E731
-    x = x + blk.ls1.gamma.float() * _ref_attention(blk.attn, ln(blk.norm1, x), pos)
+    x = x + blk.ls1.gamma.float() * _ref_attention(blk.attn, ln(blk.norm1, x), pos, sparse)
     h = F.gelu(F.linear(ln(blk.norm2, x), blk.mlp.fc1.weight.float(), blk.mlp.fc1.bias.float()))
     return x + blk.ls2.gamma.float() * F.linear(h, blk.mlp.fc2.weight.float(), blk.mlp.fc2.bias.float())
 
 
-def _ref_aggregator(agg, images):
+def _ref_aggregator(agg, images, lists=None):
     from vasc_amd.aggregator import grid_positions
     B, N, _, Hi, Wi = images.shape
     x = ((images - agg._resnet_mean) / agg._resnet_std).view(B * N, 3, Hi, Wi).float()
@@ -64,10 +102,76 @@ def _ref_aggregator(agg, images):
     tok = torch.cat([*(s.float() for s in special), tok], dim=1)
     P, C = tok.shape[1:]
     pos = grid_positions(B * N, Hi // agg.patch_size, Wi // agg.patch_size, agg.patch_start_idx, images.device)
+    S = agg.patch_start_idx
     for i in range(agg.aa_block_num):
         tok = _ref_block(agg.frame_blocks[i], tok.view(B * N, P, C), pos)
-        tok = _ref_block(agg.global_blocks[i], tok.view(B, N * P, C), pos.reshape(B, N * P, 2))
+        sparse = None if lists is None else (N, P, S, lists[i]["index"], lists[i]["count"])
+        tok = _ref_block(agg.global_blocks[i], tok.view(B, N * P, C), pos.reshape(B, N * P, 2), sparse)
     return tok.view(B, N, P, C)
+
+
+def _ref_pi3(model, images, lists=None):
+    """float32 restatement of Pi3Decoder.forward (odd blocks global)."""
+    from vasc_amd.aggregator import grid_positions
+    B, N, _, Hi, Wi = images.shape
+    x = images.view(B * N, 3, Hi, Wi).float()
+    hid = F.conv2d(x, model.patch_embed.weight.float(), model.patch_embed.bias.float(), stride=model.patch_size)
+    hid = hid.flatten(2).transpose(1, 2)
+    reg = model.register_token.float().repeat(B, N, 1, 1).reshape(B * N, *model.register_token.shape[-2:])
+    hid = torch.cat([reg, hid], dim=1)
+    P, C = hid.shape[1:]
+    S = model.patch_start_idx
+    pos = grid_positions(B * N, Hi // model.patch_size, Wi // model.patch_size, S, images.device)
+    final, g = [], 0
+    for i, blk in enumerate(model.decoder):
+        if i % 2 == 0:
+            hid = _ref_block(blk, hid.reshape(B * N, P, C), pos)
+        else:
+            sparse = None if lists is None else (N, P, S, lists[g]["index"], lists[g]["count"])
+            hid = _ref_block(blk, hid.reshape(B, N * P, C), pos.reshape(B, N * P, 2), sparse)
+            g += 1
+        if i + 1 in (len(model.decoder) - 1, len(model.decoder)):
+            final.append(hid.reshape(B * N, P, C))
+    return torch.cat(final, dim=-1)
+
+
+class _Recorder:
+    """Records, per sparse global layer, the pooled scores, the value tensor
+    and the index lists that the selection produced."""
+
+    def __init__(self, monkeypatch):
+        from vasc_amd import sparse_wrapper
+        self.layers = []
+        original = sparse_wrapper._select_for_layer
+
+        def record(key, value, pooled_score, *args, **kwargs):
+            sel, total = original(key, value, pooled_score, *args, **kwargs)
+            self.layers.append({"prob": pooled_score.clone(), "value": value.clone(),
+                                "index": sel["index"].clone(), "count": sel["count"].clone()})
+            return sel, total
+
+        monkeypatch.setattr(sparse_wrapper, "_select_for_layer", record)
+
+
+def _oracle_chain(layers, n_patch, n_total, ratios, mode, official):
+    """The recorded lists vs the oracle selection chain on the recorded scores."""
+    from oracle import selector as OS
+    from vasc_amd import ops
+    state: dict = {}
+    for li, rec in enumerate(layers):
+        iota = None
+        if mode == "vasc":
+            iota = ops.pool_qkv(v=rec["value"][..., :n_patch, :])[3].cpu().numpy()
+        final, _ = OS.layer_selection(rec["prob"].cpu().numpy(), mode=mode, sparse_ratio=ratios[li],
+                                      patch_tokens=n_patch, total_tokens=n_total, official_mask=official,
+                                      state=state, layer_idx=li, iota=iota)
+        idx, cnt = OS.index_lists(final)
+        got_i, got_c = rec["index"].cpu().numpy(), rec["count"].cpu().numpy()
+        assert np.array_equal(got_c, cnt), f"layer {li}: counts differ from the oracle"
+        for r in range(cnt.size):
+            n = cnt.reshape(-1)[r]
+            a = got_i.reshape(-1, got_i.shape[-1])[r, :n]
+            assert np.array_equal(a, idx.reshape(-1, idx.shape[-1])[r, :n]), f"layer {li}: row {r}"
 
 
 def _close(out, ref):
@@ -143,3 +247,47 @@ def test_pi3_decoder_topk_runs_and_zero_sparsity_is_dense():
             sparse, _ = model(images)
     assert pos.shape == (3, 35, 2)
     _close(sparse, dense.float())
+
+
+def test_vasc_aggregator_matches_torch_float32_on_its_lists(monkeypatch):
+    """VGGT-shaped aggregator in vasc mode with the structural-style per-layer
+    ratios: output vs the float32 restatement over the recorded lists, and the
+    lists vs the oracle's VASC chain (official mask: no forced tail)."""
+    agg = _model(Aggregator, dim=128, depth=3, num_heads=2, mlp_ratio=2.0, intermediate_layer_idx=(2,))
+    images = _images(N=6, H=112, W=126)
+    ratios = [0.75, 0.6, 0.8]
+    rec = _Recorder(monkeypatch)
+    with torch.no_grad():
+        agg = agg.to(torch.bfloat16)
+        with _Env("vggt", "vasc"):
+            install.sparse_aggregator_from_vggt_layerwise(agg, layer_sparsity_ratios=ratios, verbose=False)
+            outs, _ = agg(images)
+        assert len(rec.layers) == 3
+        P = 5 + 8 * 9
+        _oracle_chain(rec.layers, 6 * (P - 5), 6 * P, ratios, "vasc", official=True)
+        for r in rec.layers:  # the lists are sparse: some blocks left out in every layer
+            assert int(r["count"].sum()) < r["count"].numel() * (-(-6 * P // 64))
+        ref = _ref_aggregator(agg, images, rec.layers)
+    _close(outs[-1][..., 128:], ref)
+
+
+@pytest.mark.parametrize("mode", ["vasc", "topk"])
+def test_pi3_decoder_sparse_matches_torch_float32_on_its_lists(mode, monkeypatch):
+    """Pi3-shaped decoder (6 blocks, odd ones global, 5 register tokens, the
+    mixed tail protected): output vs the float32 restatement over the recorded
+    lists, lists vs the oracle chain; dense vs the restatement without lists."""
+    model = _model(Pi3Decoder, dim=128, depth=6, num_heads=2, mlp_ratio=2.0).to(torch.bfloat16)
+    images = _images(N=5, H=98, W=126, seed=3)
+    P = 5 + 7 * 9
+    rec = _Recorder(monkeypatch)
+    with torch.no_grad():
+        dense, _ = model(images)
+        _close(dense, _ref_pi3(model, images))
+        with _Env("pi3", mode):
+            install.sparse_model_from_pi3(model, sparse_ratio=0.75, verbose=False)
+            sparse, _ = model(images)
+        assert len(rec.layers) == 3
+        _oracle_chain(rec.layers, 5 * (P - 5), 5 * P, [0.75] * 3, mode, official=False)
+        ref = _ref_pi3(model, images, rec.layers)
+    _close(sparse, ref)
+

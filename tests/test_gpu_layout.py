@@ -193,3 +193,95 @@ def test_global_layer_sparse_matches_oracle_layer():
         ref = m.proj(o).float()
     err = (out.float() - ref).abs()
     assert err.max() < 6e-2 and err.mean() < 6e-3, (err.max().item(), err.mean().item())
+
+
+@pytest.mark.parametrize("backbone", ["vggt", "pi3"])
+def test_global_layer_vasc_chain_matches_oracle(backbone, monkeypatch):
+    """Three chained global layers through adaptive_sparse_attention_forward in
+    the release vasc mode, sharing one routing_state (the cross-layer ledger).
+    Each layer's index lists are bit-exact with the oracle's VASC selector
+    chain fed the layer's GPU pooled scores and innovations (VGGT: official
+    mask; Pi3: the mixed tail block forced and protected), and each layer's
+    output matches the oracle layer (norms, rotary, reorder, attention over
+    those lists, special queries over every key, restore) through proj."""
+    import os
+    from oracle import selector as OS
+    from vasc_amd import launcher, ops, sparse_wrapper
+    from vasc_amd.aggregator import Attention, RotaryPositionEmbedding2D
+    from vasc_amd.attention import adaptive_sparse_attention_forward
+
+    recorded = []
+    original = sparse_wrapper._select_for_layer
+
+    def record(key, value, pooled_score, *args, **kwargs):
+        sel, total = original(key, value, pooled_score, *args, **kwargs)
+        recorded.append({"prob": pooled_score.clone(), "value": value.clone(), "index": sel["index"].clone(),
+                         "count": sel["count"].clone()})
+        return sel, total
+
+    monkeypatch.setattr(sparse_wrapper, "_select_for_layer", record)
+    torch.manual_seed(41)
+    N, Hp, Wp, S, heads, dim = 4, 11, 13, 5, 4, 256
+    P = Hp * Wp + S
+    n_patch, n_total = N * (P - S), N * P
+    assert n_patch % 64 != 0  # a mixed tail block
+    ys, xs = torch.meshgrid(torch.arange(Hp), torch.arange(Wp), indexing="ij")
+    frame_pos = torch.cat([torch.zeros(S, 2, dtype=torch.long), torch.stack([ys.reshape(-1), xs.reshape(-1)], -1) + 1])
+    pos = frame_pos.repeat(N, 1).unsqueeze(0).cuda()
+    rope = RotaryPositionEmbedding2D()
+    mods, xs_in, outs = [], [], []
+    routing_state: dict = {}
+    saved = {kk: os.environ.pop(kk) for kk in list(os.environ) if kk.startswith("SPARSE_VGGT_")}
+    try:
+        os.environ.update(launcher.method_environment(backbone, "vasc"))
+        official = backbone == "vggt"
+        with torch.no_grad():
+            for layer in range(3):
+                m = Attention(dim, heads, rope=rope).cuda().to(torch.bfloat16)
+                m.q_norm.weight.normal_(1.0, 0.2)
+                m.k_norm.bias.normal_(0.0, 0.2)
+                x = torch.randn(1, n_total, dim, device="cuda", dtype=torch.bfloat16)
+                outs.append(adaptive_sparse_attention_forward(m, x, pos, sparse_ratio=0.5, num_special_tokens=S,
+                                                              num_heads=heads, layer_idx=layer,
+                                                              routing_state=routing_state))
+                mods.append(m)
+                xs_in.append(x)
+    finally:
+        for kk in [kk for kk in os.environ if kk.startswith("SPARSE_VGGT_")]:
+            del os.environ[kk]
+        os.environ.update(saved)
+    assert len(recorded) == 3
+    state: dict = {}
+    bf = lambda a: torch.from_numpy(a).to(torch.bfloat16).float().numpy()  # noqa: E731
+    for layer, (rec, m, x, out) in enumerate(zip(recorded, mods, xs_in, outs)):
+        _, _, _, iota = ops.pool_qkv(v=rec["value"][..., :n_patch, :])
+        final, _ = OS.layer_selection(rec["prob"].cpu().numpy(), mode="vasc", sparse_ratio=0.5, patch_tokens=n_patch,
+                                      total_tokens=n_total, official_mask=official, state=state, layer_idx=layer,
+                                      iota=iota.cpu().numpy())
+        idx, cnt = OS.index_lists(final)
+        got_i, got_c = rec["index"].cpu().numpy(), rec["count"].cpu().numpy()
+        assert np.array_equal(got_c, cnt), f"layer {layer}: counts differ from the oracle"
+        for r, (a, b) in enumerate(zip(got_i.reshape(-1, got_i.shape[-1]), idx.reshape(-1, idx.shape[-1]))):
+            n = cnt.reshape(-1)[r]
+            assert np.array_equal(a[:n], b[:n]), f"layer {layer}: index list of row {r} differs from the oracle"
+        if not official:
+            kb = rec["prob"].shape[-1]
+            assert (got_i == kb - 1).any(-1).all(), "the protected mixed tail block is in every list"
+        with torch.no_grad():
+            qkv = m.qkv(x)
+            cos, sin = m.rope.tables(dim // heads, "cuda")
+            qp, qsp, kre, vre = OL.pack_layer(
+                qkv.float().cpu().numpy(), N, P, S, heads,
+                q_norm=(m.q_norm.weight.float().cpu().numpy(), m.q_norm.bias.float().cpu().numpy(), m.q_norm.eps),
+                k_norm=(m.k_norm.weight.float().cpu().numpy(), m.k_norm.bias.float().cpu().numpy(), m.k_norm.eps),
+                pos=pos[0].cpu().numpy(), tables=(cos.cpu().numpy(), sin.cpu().numpy()))
+        o_p = OA.block_sparse_attention(bf(qp), bf(kre), bf(vre), got_i, got_c)
+        dl, dc = OA.dense_lists(1, heads, N * S, n_total)
+        o_s = OA.block_sparse_attention(bf(qsp), bf(kre), bf(vre), dl, dc)
+        o = OL.restore_to_frame_major(np.concatenate([o_p, o_s], axis=2), N, P, S)
+        o = torch.from_numpy(o.transpose(0, 2, 1, 3).reshape(1, n_total, dim)).to(torch.bfloat16).cuda()
+        with torch.no_grad():
+            ref = m.proj(o).float()
+        err = (out.float() - ref).abs()
+        assert err.max() < 6e-2 and err.mean() < 6e-3, (layer, err.max().item(), err.mean().item())
+    assert "cosa_value_risk_pair_debt" in routing_state

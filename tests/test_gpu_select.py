@@ -156,6 +156,9 @@ def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=
     # every register-row width of the arrival pass (16 to 64 elements per lane) and, past
     # 4096 key blocks, the LDS-row arrival kernel
     (1501, 5, True, 2.0, None), (2047, 6, False, 3.0, None), (2304, 3, True, 1.0, None), (5001, 4, True, 2.0, None),
+    # the widest select instance (rows above 6144 key blocks, about 144 KB of LDS) up to the built
+    # maximum, where the arrival's float64 column partials fill all 16 slots per thread
+    (6200, 4, False, 2.0, None), (8192, 3, True, 2.0, None),
 ])
 def test_vasc_chain_bit_exact(K, Q, force_last, peak, levels):
     topk = max(int(K * 0.25), 1)

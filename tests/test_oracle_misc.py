@@ -72,6 +72,11 @@ def test_block_sparse_attention_matches_masked_sdpa():
     ref = torch.nn.functional.scaled_dot_product_attention(
         *(torch.from_numpy(t) for t in (q, k, v)), attn_mask=torch.from_numpy(full))
     np.testing.assert_allclose(out, ref.numpy(), atol=1e-10)
+    # sampled query blocks: those rows equal the full result, every other row is zero
+    part = OA.block_sparse_attention(q, k, v, idx, cnt, q_blocks=[2, 0, 2])
+    rows = np.r_[0:128, 256:300]
+    np.testing.assert_array_equal(part[:, :, rows], out[:, :, rows])
+    assert not part[:, :, 128:256].any()
 
 
 def test_dense_lists_equal_unmasked_attention():
