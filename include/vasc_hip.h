@@ -167,6 +167,39 @@ int vasc_select_blocks(const float *score, const float *innovation,
                        int32_t *count_out, void *workspace,
                        size_t workspace_bytes, void *stream);
 
+/* Largest workspace (bytes) vasc_select_blocks_noalloc can serve. */
+#define VASC_SELECT_SCRATCH_BYTES (32u << 20)
+
+/*
+ * vasc_select_blocks without a workspace argument: it allocates nothing
+ * (no hipMalloc, hipFree or allocating library call) and takes its scratch
+ * from a 32 MiB array of device memory inside the library, one copy per
+ * GPU, held until the process ends. No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, results
+ * and errors as vasc_select_blocks; sizes whose workspace
+ * (vasc_select_workspace_size) exceeds VASC_SELECT_SCRATCH_BYTES are
+ * rejected with VASC_ERR_ARGUMENT (at B = 1, H = 16: up to 4096 key blocks
+ * with 2048 query blocks). Every call on one GPU shares that GPU's scratch:
+ * calls that overlap in time on one GPU (other streams, other threads) race
+ * and must be serialised by the caller. The first call on a device resolves
+ * the scratch address with that device current.
+ */
+int vasc_select_blocks_noalloc(const float *score, const float *innovation,
+                               int64_t B, int64_t H, int64_t Q, int64_t K,
+                               int32_t mode, int32_t topk,
+                               const int32_t *row_cap,
+                               const uint8_t *protected_mask,
+                               int32_t force_last, int32_t max_capacity,
+                               int32_t sink_blocks, const float *debt_in,
+                               const float *pending_arrival,
+                               const float *prev_service, float *debt_out,
+                               float *arrival_out, float *service_out,
+                               int32_t *gate_out, float *priority_out,
+                               uint8_t *mask_out, int32_t *index_out,
+                               int64_t width, int32_t *count_out,
+                               void *stream);
+
 /*
  * Terminal ledger settlement (finalize_cosa_value_risk_pair_debt,
  * sparse_wrapper.py:4101-4177): debt_out = max(debt_in + pending - service, 0)

@@ -35,6 +35,8 @@ SIGNATURES: dict[str, tuple] = {
     "vasc_select_workspace_size": (c_size_t, [I64, I64, I64, I64]),
     "vasc_select_blocks": (c_int32, [P, P, I64, I64, I64, I64, I32, I32, P, P, I32, I32, I32,
                                      P, P, P, P, P, P, P, P, P, P, I64, P, P, c_size_t, P]),
+    "vasc_select_blocks_noalloc": (c_int32, [P, P, I64, I64, I64, I64, I32, I32, P, P, I32, I32, I32,
+                                             P, P, P, P, P, P, P, P, P, P, I64, P, P]),
     "vasc_settle_terminal": (c_int32, [P, P, P, I64, P, P]),
     "vasc_cdf_counts": (c_int32, [P, I64, I64, I64, I64, P, I32, I32, P, P, P]),
     "vasc_packed_v_elems": (c_int64, [I64, I64, I64, I64]),

@@ -35,6 +35,7 @@
 // Top-K mode runs the select launch alone.
 #pragma clang fp contract(off)
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1405,6 +1406,40 @@ int select_blocks_impl(const float *score, const float *innovation, int64_t B, i
   return launch_rows(p, vasc, reinterpret_cast<hipStream_t>(stream));
 }
 
+// Scratch of vasc_select_blocks_noalloc: one copy per GPU, held for the
+// process lifetime. Every kernel writes each workspace word it later reads
+// within the same call (the pair counts are cleared by the head pass), so
+// nothing has to start at zero and no call depends on an earlier one.
+static __device__ __align__(256) char scratch[VASC_SELECT_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, once resolved
+
+// Device address of the current device's scratch, resolved with
+// hipGetSymbolAddress on the first call on that device (with it current).
+int scratch_for_current_device(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("vasc_select_blocks_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return VASC_ERR_HIP;
+  }
+  VASC_SUPPORTED(dev >= 0 && dev < kMaxDevices, "device %d outside the %d supported", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("vasc_select_blocks_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+      return VASC_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return VASC_OK;
+}
+
 }  // namespace
 }  // namespace vasc
 
@@ -1420,6 +1455,35 @@ extern "C" int vasc_select_blocks(const float *score, const float *innovation, i
                                   max_capacity, sink_blocks, debt_in, pending_arrival, prev_service, debt_out,
                                   arrival_out, service_out, gate_out, priority_out, mask_out, index_out, width,
                                   count_out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int vasc_select_blocks_noalloc(const float *score, const float *innovation, int64_t B, int64_t H,
+                                          int64_t Q, int64_t K, int32_t mode, int32_t topk, const int32_t *row_cap,
+                                          const uint8_t *protected_mask, int32_t force_last, int32_t max_capacity,
+                                          int32_t sink_blocks, const float *debt_in, const float *pending_arrival,
+                                          const float *prev_service, float *debt_out, float *arrival_out,
+                                          float *service_out, int32_t *gate_out, float *priority_out,
+                                          uint8_t *mask_out, int32_t *index_out, int64_t width, int32_t *count_out,
+                                          void *stream) {
+  using namespace vasc;
+  void *ws = nullptr;
+  size_t bytes = 0;
+  if (mode == VASC_MODE_VASC) {
+    VASC_REQUIRE(B > 0 && H > 0 && Q > 0 && K > 0, "sizes must be positive");
+    VASC_SUPPORTED(K <= 8192, "K=%lld key blocks not built (built: <= 8192)", (long long)K);
+    const size_t need = layout(B, H, Q, K).bytes;
+    VASC_REQUIRE(need <= static_cast<size_t>(VASC_SELECT_SCRATCH_BYTES),
+                 "vasc_select_blocks_noalloc: these sizes need %zu bytes of scratch, above the built maximum of "
+                 "%zu (VASC_SELECT_SCRATCH_BYTES); use vasc_select_blocks with a caller workspace",
+                 need, static_cast<size_t>(VASC_SELECT_SCRATCH_BYTES));
+    int rc;
+    if ((rc = scratch_for_current_device(&ws))) return rc;
+    bytes = VASC_SELECT_SCRATCH_BYTES;
+  }
+  return select_blocks_impl(score, innovation, B, H, Q, K, mode, topk, row_cap, protected_mask, force_last,
+                            max_capacity, sink_blocks, debt_in, pending_arrival, prev_service, debt_out, arrival_out,
+                            service_out, gate_out, priority_out, mask_out, index_out, width, count_out, ws, bytes,
+                            stream);
 }
 
 extern "C" int vasc_settle_terminal(const float *debt_in, const float *pending_arrival, const float *service,
