@@ -1,18 +1,28 @@
 #!/usr/bin/env python3
 """Benchmark of the VASC sparse global-attention path on one MI355X.
 
-Workload (the metric's configuration): the 24 global
-attention layers of a VGGT-shaped aggregator at 32 frames x 1041 tokens
-(33 312 tokens, 16 heads, head_dim 64), mode vasc, sparsity 0.75 with the
-structural layer-budget profile. One step = the sparse op (pooling +
-pooled softmax, VASC selection with the cross-layer ledger, V pack,
-block-sparse MFMA attention) of all 24 layers over one batch of synthetic
-Q/K/V resident in HBM, ledger cleared at the start of the step as the
-reference clears its routing_state per forward.
+Headline (the metric's configuration): frames/s of
+the VGGT-shaped aggregator forward (24 frame + 24 global blocks, dim 1024,
+16 heads, MLP 4096, random-init bf16) on 32 frames of 392x518 uniform noise
+(33 312 global tokens), mode vasc at sparsity 0.75 with the structural
+layer-budget profile. One step = one aggregator forward; ``value`` = 32 /
+forward seconds. Beside it:
 
-Prints one JSON line (the driver's contract) with ``value`` = frames/s of
-the 24 global-attention ops, the attention kernel's roofline and the CPU
-baseline. Progress goes to stderr.
+* the global layer in the reference's timer scope (qkv, layout, sparse op,
+  restore, proj; median over the timed forwards) and the same for dense;
+* the roofline of the dominant kernel, the block-sparse attention launch of
+  the global layers, timed with hipEvents around each launch inside the
+  timed forwards;
+* the 24-layer sparse op alone on synthetic Q/K/V (pool + pooled softmax,
+  VASC selection with the cross-layer ledger, V pack, attention) with
+  per-kernel HBM rates and the dense-attention comparison;
+* the CPU baseline (torch fp32 restatements of the reference's dense and
+  topk paths on this host's cores).
+
+Prints one JSON line (the driver's contract). Progress goes to stderr.
+Other workloads: ``--workload c3`` (128 frames, s=0.875), ``c4`` (the
+Pi3-shaped decoder at 64 frames), ``c5`` (kernel microbenchmarks);
+``--probe`` runs untimed programs for rocprofv3 counter passes.
 """
 from __future__ import annotations
 
@@ -128,7 +138,8 @@ def run_step(layers, ratios, ledger, timer, keep=None):
 def attention_min_bytes(index, count, n_q, n_k, d):
     """Least HBM bytes one sparse-attention launch can move: Q read and O written
     once, plus every K block and packed V tile that some query block of the
-    head selects, each read once (bf16)."""
+    head selects, each read once (bf16). Returns (bytes, distinct key blocks
+    listed per head)."""
     kb = -(-n_k // 64)
     width = index.shape[-1]
     valid = torch.arange(width, device=index.device) < count.unsqueeze(-1).long()
@@ -137,7 +148,7 @@ def attention_min_bytes(index, count, n_q, n_k, d):
     touched.scatter_(2, idx, True)
     blocks = int(touched[..., :kb].sum().item())
     heads = index.shape[0] * index.shape[1]
-    return heads * n_q * d * 2 * 2 + blocks * 64 * d * 2 * 2
+    return heads * n_q * d * 2 * 2 + blocks * 64 * d * 2 * 2, blocks / heads
 
 
 def hbm_bytes_per_launch(H, n_patch, n_total, d, listed_per_layer):
@@ -256,182 +267,197 @@ def run_c5(dev) -> int:
     return 0
 
 
-def run_aggregator(dev, frames: int, ratios, reps: int = 5, warmup: int = 2) -> dict:
-    """C2's VGGT-shaped aggregator (24 frame + 24 global blocks, dim 1024, 16
-    heads, MLP 4096, random init bf16) on seeded uniform-noise images
-    ``[1, frames, 3, 392, 518]``: dense (every global block on the dense MFMA
-    kernel) and vasc with the structural profile. Reports the forward time
-    (frames/s = frames / forward seconds) and, as the reference's
-    CudaAttentionTimer does (eval_7scenes_sparse_vggt.py:1533-1574), hipEvents
-    around every global attention module (qkv, layout, sparse op, restore,
-    proj), summed per forward."""
-    from vasc_amd import install
-    from vasc_amd.aggregator import Aggregator
-    from vasc_amd.launcher import method_environment
+class AttnLaunchEvents:
+    """hipEvents around every ``ops.global_attn`` launch (the sparse global
+    layers' attention kernel) on the stream it is launched on, plus the
+    lists of each layer's latest launch for its algorithmic flops."""
 
-    torch.manual_seed(0)
+    def __init__(self, layers: int):
+        self.layers = layers
+        self.events: list = []
+        self.lists: dict = {}
+        self.enabled = False
+
+    def __enter__(self):
+        from vasc_amd import ops
+        self._ops = ops
+        self._orig = ops.global_attn
+
+        def timed(q_patch, q_special, k, vt, index, count, **kw):
+            if not self.enabled:
+                return self._orig(q_patch, q_special, k, vt, index, count, **kw)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            out = self._orig(q_patch, q_special, k, vt, index, count, **kw)
+            b.record()
+            self.events.append((a, b))
+            n_special = 0 if q_special is None else q_special.shape[2]
+            self.lists[len(self.events) % self.layers] = (index, count, q_patch.shape[2], k.shape[2], n_special,
+                                                          q_patch.shape[1], q_patch.shape[3])
+            return out
+
+        ops.global_attn = timed
+        return self
+
+    def __exit__(self, *exc):
+        self._ops.global_attn = self._orig
+
+    def mean_ms(self) -> float:
+        return statistics.fmean(a.elapsed_time(b) for a, b in self.events)
+
+    def flops_per_launch(self) -> float:
+        """Mean algorithmic flops of one launch: 4*d per (query, key) pair of
+        the listed blocks, plus the special queries over every key."""
+        from vasc_amd import pipeline
+        tot = 0.0
+        for index, count, n_patch, n_total, n_special, H, D in self.lists.values():
+            tot += pipeline.attention_flops((index, count), n_patch, n_total, D)
+            tot += 4.0 * D * H * n_special * n_total * index.shape[0]
+        return tot / len(self.lists)
+
+
+def build_aggregator(dev, seed: int = 0):
+    from vasc_amd.aggregator import Aggregator
+    torch.manual_seed(seed)
     with torch.device(dev):
         agg = Aggregator(dim=1024, depth=24, num_heads=16, mlp_ratio=4.0)
-    agg = agg.to(torch.bfloat16).eval()
+    return agg.to(torch.bfloat16).eval()
+
+
+class _ModeEnv:
+    """The reference's SPARSE_VGGT_* switches of one release mode."""
+
+    def __init__(self, backbone, mode):
+        from vasc_amd.launcher import method_environment
+        self.env = method_environment(backbone, mode)
+
+    def __enter__(self):
+        self.saved = {k: os.environ.pop(k) for k in list(os.environ) if k.startswith("SPARSE_VGGT_")}
+        os.environ.update(self.env)
+
+    def __exit__(self, *exc):
+        for k in [k for k in os.environ if k.startswith("SPARSE_VGGT_")]:
+            del os.environ[k]
+        os.environ.update(self.saved)
+
+
+def run_aggregator(dev, frames: int, ratios, steps: int, warmup: int, dense_reps: int = 3) -> dict:
+    """The VGGT-shaped aggregator (24 frame + 24 global blocks, dim 1024, 16
+    heads, MLP 4096, random init bf16) on seeded uniform-noise images
+    ``[1, frames, 3, 392, 518]``.
+
+    * dense: every global block on the dense MFMA kernel (``dense_reps``
+      forwards after one warm-up);
+    * vasc with the per-layer ratios: ``warmup`` forwards, then exactly
+      ``steps`` forwards timed between two synchronizations (the headline),
+      with hipEvents around every global attention module (the reference's
+      CudaAttentionTimer scope, eval_7scenes_sparse_vggt.py:1533-1574: qkv,
+      layout, sparse op, restore, proj) and around every attention launch
+      (the roofline's kernel).
+    """
+    from vasc_amd import install
+    agg = build_aggregator(dev)
     g = torch.Generator(device=dev).manual_seed(0)
     images = torch.rand(1, frames, 3, 392, 518, device=dev, generator=g)
-    events: list = []
+    layer_events: list = []
 
     def pre(mod, args, kwargs=None):
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
-        events.append([ev, None])
+        layer_events.append([ev, None])
 
     def post(mod, args, out):
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
-        events[-1][1] = ev
+        layer_events[-1][1] = ev
 
     for blk in agg.global_blocks:
         blk.attn.register_forward_pre_hook(pre)
         blk.attn.register_forward_hook(post)
+    L = len(agg.global_blocks)
 
-    def measure(tag):
-        fwd, attn = [], []
+    def forwards(n, timed):
+        """n forwards; returns (total ms between synchronizations, per-forward
+        global-layer ms)."""
+        layer_events.clear()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
         with torch.no_grad():
-            for i in range(warmup + reps):
-                events.clear()
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record()
+            for _ in range(n):
                 agg(images)
-                b.record()
-                torch.cuda.synchronize()
-                if i >= warmup:
-                    fwd.append(a.elapsed_time(b))
-                    attn.append(sum(x.elapsed_time(y) for x, y in events))
-        f, t = statistics.median(fwd), statistics.median(attn)
-        log(f"aggregator {tag}: forward {f:.2f} ms ({frames / (f * 1e-3):.1f} frames/s), "
-            f"24 global attention layers {t:.2f} ms ({t / len(agg.global_blocks):.3f} ms/layer)")
-        return {"forward_ms": f, "frames_per_s": frames / (f * 1e-3), "global_attn_ms_per_forward": t,
-                "global_layer_ms": t / len(agg.global_blocks), "frames_per_s_global_layers": frames / (t * 1e-3)}
+        b.record()
+        torch.cuda.synchronize()
+        per_fwd = [sum(x.elapsed_time(y) for x, y in layer_events[i * L:(i + 1) * L]) for i in range(n)]
+        return a.elapsed_time(b), per_fwd
 
-    out = {"dense": measure("dense")}
-    saved = {k: os.environ.pop(k) for k in list(os.environ) if k.startswith("SPARSE_VGGT_")}
-    os.environ.update(method_environment("vggt", "vasc"))
-    try:
+    out = {}
+    forwards(1, False)
+    total, glob = forwards(dense_reps, True)
+    out["dense"] = {"forward_ms": total / dense_reps, "frames_per_s": frames / (total / dense_reps * 1e-3),
+                    "global_attn_ms_per_forward": statistics.median(glob),
+                    "global_layer_ms": statistics.median(glob) / L}
+    log(f"aggregator dense: forward {out['dense']['forward_ms']:.2f} ms, "
+        f"global layer {out['dense']['global_layer_ms']:.3f} ms")
+
+    with _ModeEnv("vggt", "vasc"), AttnLaunchEvents(L) as attn_ev:
         install.sparse_aggregator_from_vggt_layerwise(agg, layer_sparsity_ratios=ratios, verbose=False)
-        out["vasc"] = measure("vasc")
-    finally:
-        for k in [k for k in os.environ if k.startswith("SPARSE_VGGT_")]:
-            del os.environ[k]
-        os.environ.update(saved)
-    out["speedup_global_layers_vs_dense"] = out["dense"]["global_attn_ms_per_forward"] / \
-        out["vasc"]["global_attn_ms_per_forward"]
-    out["config"] = ("VGGT-shaped aggregator, random-init bf16, 14x14 conv patch embedding, "
-                     f"{frames} frames of 392x518 uniform noise, vasc with the structural profile")
-    del agg
+        log(f"aggregator vasc: {warmup} warm-up forwards, {steps} timed")
+        forwards(warmup, False)
+        attn_ev.enabled = True
+        total, glob = forwards(steps, True)
+        attn_ev.enabled = False
+        fwd_ms = total / steps
+        out["vasc"] = {"forward_ms": fwd_ms, "frames_per_s": frames / (fwd_ms * 1e-3),
+                       "global_attn_ms_per_forward": statistics.median(glob),
+                       "global_layer_ms": statistics.median(glob) / L,
+                       "frames_per_s_global_layers": frames / (statistics.median(glob) * 1e-3)}
+        out["attn_ms_per_launch"] = attn_ev.mean_ms()
+        out["attn_launches"] = len(attn_ev.events)
+        out["attn_flops_per_launch"] = attn_ev.flops_per_launch()
+        counts = [c for _, c, *_ in attn_ev.lists.values()]
+        out["mean_listed_blocks_per_row"] = float(torch.stack([c.float().mean() for c in counts]).mean())
+    log(f"aggregator vasc: forward {fwd_ms:.2f} ms ({out['vasc']['frames_per_s']:.1f} frames/s), global layer "
+        f"{out['vasc']['global_layer_ms']:.3f} ms, attention {out['attn_ms_per_launch']:.3f} ms/launch")
+    out["speedup_global_layers_vs_dense"] = out["dense"]["global_layer_ms"] / out["vasc"]["global_layer_ms"]
+    del agg, images
     torch.cuda.empty_cache()
     return out
 
 
-def cpu_baseline(layer, ratio, frames, n_layers):
-    from oracle import cpu_baseline as cb
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    q, k, v = (t.float().cpu() for t in layer)
-    log(f"cpu baseline: one C2 layer, torch fp32 on {cores} threads")
-    t0 = time.perf_counter()
-    cb.topk_layer(q, k, v, ratio)
-    dt = time.perf_counter() - t0
-    return {
-        "value": frames / (dt * n_layers),
-        "unit": "frames/s",
-        "cores": cores,
-        "kind": "port",
-        "layer_s": dt,
-        "sample": (f"1 of {n_layers} C2 global layers (layer 0, s={ratio:.4f}), Top-K path "
-                   f"(pooled predictor + top-k + block-gathered attention), torch CPU fp32, single shot, "
-                   f"scaled x{n_layers}"),
-    }
-
-
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=("c2", "c3", "c5"), default="c2",
-                    help="c2: the metric's configuration (default); c3: 128 frames at s=0.875; "
-                         "c5: per-kernel microbenchmarks at T = 16k/64k/256k (one JSON line per case)")
-    ap.add_argument("--frames", type=int, default=None)
-    ap.add_argument("--sparsity", type=float, default=None)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-dense", action="store_true")
-    ap.add_argument("--no-aggregator", action="store_true",
-                    help="skip the VGGT-shaped aggregator forward (global-layer ms in the reference's timer scope)")
-    ap.add_argument("--graph", dest="graph", action="store_true", default=True,
-                    help="replay the step as a HIP graph (default)")
-    ap.add_argument("--no-graph", dest="graph", action="store_false")
-    ap.add_argument("--traffic-probe", action="store_true",
-                    help="untimed: a 256 MiB copy (counter calibration) then one eager step, for rocprofv3 --pmc")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the sparse op would shard by head, one head group per GPU). Run with --gpus 1.", file=sys.stderr)
-        return 2
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU", file=sys.stderr)
-        return 2
-
+def run_sparse_op(dev, N: int, ratios, steps: int, warmup: int, graph_mode: bool, dense: bool) -> dict:
+    """The 24 global layers' sparse op alone (pool + pooled softmax, VASC
+    selection with the chained ledger, V pack, block-sparse attention) on
+    synthetic Q/K/V resident in HBM: eager steps with hipEvents per kernel,
+    then the same step replayed as a HIP graph (checked bit-exact against the
+    eager step three times, with eager work in between)."""
     from vasc_amd import ops, pipeline
-    from vasc_amd.launcher import layer_sparsity
-
-    dev = torch.device("cuda:0")
-    if args.workload == "c5":
-        return run_c5(dev)
-    defaults = {"c2": (32, 0.75), "c3": (128, 0.875)}[args.workload]
-    args.frames = defaults[0] if args.frames is None else args.frames
-    args.sparsity = defaults[1] if args.sparsity is None else args.sparsity
-    if args.workload == "c3":
-        args.no_cpu_baseline = True  # the CPU port needs minutes per C3 layer
-    N, P, S, H, D, L = args.frames, 1041, 5, 16, 64, 24
-    ratios = layer_sparsity("vggt", args.sparsity, "paper") or [args.sparsity] * L
-    log(f"generating {L} layers of synthetic Q/K/V ({N} frames x {P} tokens, H={H})")
+    P, S, H, D, L = 1041, 5, 16, 64, len(ratios)
+    log(f"sparse op: generating {L} layers of synthetic Q/K/V ({N} frames x {P} tokens, H={H})")
     layers = [synthetic_layer(N, P, S, H, D, seed=li, device=dev) for li in range(L)]
     torch.cuda.synchronize()
     ledger = pipeline.Ledger()
-
-    if args.traffic_probe:
-        src = torch.empty(128 * 2**20, dtype=torch.bfloat16, device=dev).normal_()
-        dst = torch.empty_like(src)
-        dst.copy_(src)  # 256 MiB read + 256 MiB written: the FETCH_SIZE / WRITE_SIZE scale
+    for _ in range(warmup):
         run_step(layers, ratios, ledger, Timer(enabled=False))
-        torch.cuda.synchronize()
-        log("traffic probe done")
-        return 0
-
-    log(f"warmup {args.warmup} steps")
-    for _ in range(args.warmup):
-        run_step(layers, ratios, ledger, Timer(enabled=False))
-    torch.cuda.synchronize()
-
-    # Eager timed region: hipEvents around every launch on the current stream.
-    log(f"timing {args.steps} eager steps")
     timer = Timer()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     host0 = time.perf_counter()
     start.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         run_step(layers, ratios, ledger, timer)
     stop.record()
-    host_enqueue_ms = (time.perf_counter() - host0) * 1e3 / args.steps
+    host_enqueue_ms = (time.perf_counter() - host0) * 1e3 / steps
     torch.cuda.synchronize()
-    eager_ms = start.elapsed_time(stop) / args.steps
-    kernel_ms = {k: v / args.steps for k, v in timer.totals_ms().items()}
-    launches = {k: v // args.steps for k, v in timer.counts().items()}
+    eager_ms = start.elapsed_time(stop) / steps
+    kernel_ms = {k: v / steps for k, v in timer.totals_ms().items()}
+    launches = {k: v // steps for k, v in timer.counts().items()}
 
-    # Algorithmic work of one step (outside the timed region).
     keep = []
     run_step(layers, ratios, ledger, Timer(enabled=False), keep)
     n_patch, n_total = N * (P - S), N * P
     attn_flops_step = sum(pipeline.attention_flops((i, c), n_patch, n_total, D) for i, c, _ in keep)
-    attn_min_bytes_step = sum(attention_min_bytes(i, c, n_patch, n_total, D) for i, c, _ in keep)
+    mins = [attention_min_bytes(i, c, n_patch, n_total, D) for i, c, _ in keep]
     listed_step = sum(int(c.sum().item()) for _, c, _ in keep)
     kernel_bytes = hbm_bytes_per_launch(H, n_patch, n_total, D, listed_step / L)
     eager_out = [o.clone() for _, _, o in keep]
@@ -439,8 +465,7 @@ def main() -> int:
     del keep
 
     ms_per_step, mode = eager_ms, "eager"
-    if args.graph:
-        log("capturing one step in a HIP graph")
+    if graph_mode:
         gkeep = []
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
@@ -459,71 +484,39 @@ def main() -> int:
                     raise RuntimeError(f"graph replay {rep} differs from the eager step")
             run_step(layers[:1], ratios, ledger, Timer(enabled=False))
             torch.cuda.synchronize()
-        log(f"timing {args.steps} graph replays")
         torch.cuda.synchronize()
         start.record()
-        for _ in range(args.steps):
+        for _ in range(steps):
             graph.replay()
         stop.record()
         torch.cuda.synchronize()
-        ms_per_step, mode = start.elapsed_time(stop) / args.steps, "hip_graph"
+        ms_per_step, mode = start.elapsed_time(stop) / steps, "hip_graph"
+        del graph, gkeep
 
     attn_ms_launch = kernel_ms["attention"] / launches["attention"]
     achieved = attn_flops_step / L / (attn_ms_launch * 1e-3) / 1e12
     dense_flops_layer = 4.0 * D * H * n_patch * n_total
-    layer_ms = ms_per_step / L
-    log(f"step {ms_per_step:.3f} ms ({mode}; eager {eager_ms:.3f} ms, host enqueue {host_enqueue_ms:.3f} ms), "
-        f"attention {attn_ms_launch:.3f} ms/layer, {achieved:.1f} TFLOP/s")
-
-    result = {
-        "metric": METRIC if args.workload == "c2" else
-        f"sparse global-attn layer ms + eff. TFLOP/s @{args.sparsity:g} sparsity, {N} frames; frames/s",
-        "value": N / (ms_per_step * 1e-3),
-        "unit": "frames/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) + per-frame rank-8 (scale 0.5) Q/K/V at the C2 global-layer shape",
-        "config": {
-            "workload": f"{args.workload.upper()} VGGT-shaped global attention: 24 layers x sparse op "
-                        "(pool+softmax, vasc select + ledger, V pack, block-sparse attention)",
-            "frames": N, "tokens": n_total, "patch_tokens": n_patch, "heads": H, "head_dim": D,
-            "layers": L, "mode": "vasc", "sparsity": args.sparsity, "structural_allocation": True,
-        },
-        "layer_ms": layer_ms,
-        "timing_mode": mode,
-        "eager_ms_per_step": eager_ms,
-        "host_enqueue_ms_per_step": host_enqueue_ms,
-        "attn_tflops": achieved,
-        "eff_tflops": dense_flops_layer / (layer_ms * 1e-3) / 1e12,
+    out = {
+        "description": "24 layers x sparse op (pool+softmax, vasc select + ledger, V pack, block-sparse attention) "
+                       "on synthetic N(0,1) + per-frame rank-8 Q/K/V",
+        "ms_per_step": ms_per_step, "frames_per_s": N / (ms_per_step * 1e-3), "timing_mode": mode,
+        "layer_ms": ms_per_step / L, "eager_ms_per_step": eager_ms, "host_enqueue_ms_per_step": host_enqueue_ms,
         "kernel_ms_per_step": kernel_ms,
         "kernels_hbm": {
             name: {"ms_per_launch": kernel_ms[name] / launches[name], "bytes_per_launch": nbytes,
                    "GB_s": nbytes / (kernel_ms[name] / launches[name] * 1e-3) / 1e9,
                    "frac_of_hbm_peak": nbytes / (kernel_ms[name] / launches[name] * 1e-3) / 1e9 / PEAK_HBM_GBS}
-            for name, nbytes in kernel_bytes.items()
-        },
-        "roofline": {
-            "kernel": "bsattn_fwd_kernel",
-            "bound": "mfma",
-            "achieved": achieved,
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": traffic_bytes() if args.workload == "c2" else None,
-            "traffic_source": TRAFFIC_SUMMARY if args.workload == "c2" else None,
-            "flops_per_launch": attn_flops_step / L,
-            "min_hbm_bytes_per_launch": attn_min_bytes_step / L,
-            "ms_per_launch": attn_ms_launch,
-        },
+            for name, nbytes in kernel_bytes.items()},
+        "attention": {"ms_per_launch": attn_ms_launch, "flops_per_launch": attn_flops_step / L,
+                      "TFLOP_s": achieved, "frac_of_mfma_peak": achieved / PEAK_BF16_TFLOPS,
+                      "min_hbm_bytes_per_launch": statistics.fmean(m[0] for m in mins),
+                      "distinct_key_blocks_per_head": statistics.fmean(m[1] for m in mins),
+                      "key_blocks_per_head": -(-n_total // 64)},
+        "dense_equivalent_TFLOP_s": dense_flops_layer / (ms_per_step / L * 1e-3) / 1e12,
     }
-
-    if not args.no_dense:
+    log(f"sparse op: step {ms_per_step:.3f} ms ({mode}; eager {eager_ms:.3f} ms), attention "
+        f"{attn_ms_launch:.3f} ms/layer, {achieved:.1f} TFLOP/s")
+    if dense:
         q, k, v = layers[0]
         vt = ops.pack_v(v)
         times = []
@@ -536,25 +529,266 @@ def main() -> int:
             if i:
                 times.append(a.elapsed_time(b))
         dense_ms = statistics.median(times)
-        result["dense_attn_ms"] = dense_ms
-        result["dense_tflops"] = dense_flops_layer / (dense_ms * 1e-3) / 1e12
-        result["speedup_vs_dense"] = dense_ms / layer_ms
-        log(f"dense attention {dense_ms:.3f} ms/layer ({result['dense_tflops']:.1f} TFLOP/s)")
+        out["dense_attn_ms"] = dense_ms
+        out["dense_attn_TFLOP_s"] = dense_flops_layer / (dense_ms * 1e-3) / 1e12
+        out["speedup_vs_dense_attention"] = dense_ms / out["layer_ms"]
+        log(f"sparse op: dense attention {dense_ms:.3f} ms/layer, speedup {out['speedup_vs_dense_attention']:.2f}x")
+    del layers
+    torch.cuda.empty_cache()
+    return out
 
-    if not args.no_aggregator and args.workload == "c2":
-        del layers
-        torch.cuda.empty_cache()
-        result["aggregator"] = run_aggregator(dev, N, ratios)
-        result["global_layer_ms"] = result["aggregator"]["vasc"]["global_layer_ms"]
 
-    if not args.no_cpu_baseline:
-        if args.no_aggregator or args.workload != "c2":
-            q0, k0, v0 = layers[0]
-        else:
-            q0, k0, v0 = synthetic_layer(N, P, S, H, D, seed=0, device=dev)
-        result["cpu_baseline"] = cpu_baseline((q0, k0, v0), ratios[0], N, L)
-        log(f"cpu baseline {result['cpu_baseline']['layer_s']:.2f} s/layer")
+def smooth_images(frames: int, seed: int, dev) -> torch.Tensor:
+    """C4's images: rand(1, frames, 3, 28, 37) bilinearly upsampled to 392x518."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    low = torch.rand(frames, 3, 28, 37, device=dev, generator=g)
+    return torch.nn.functional.interpolate(low, size=(392, 518), mode="bilinear", align_corners=False).unsqueeze(0)
 
+
+def run_c4(dev, steps: int, warmup: int) -> dict:
+    """C4: the Pi3-shaped decoder (36 blocks, odd ones global, dim 1024, 16
+    heads, 5 register tokens, no camera token, random init bf16) on 64
+    frames of seeded smooth noise: dense, then vasc and topk at sparsity 0.75
+    with the structural profile (the release default above 0.70), each
+    output compared with the dense one."""
+    from vasc_amd import install
+    from vasc_amd.aggregator import Pi3Decoder
+    from vasc_amd.launcher import allocation_settings
+    frames = 64
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Pi3Decoder(dim=1024, depth=36, num_heads=16, mlp_ratio=4.0)
+    model = model.to(torch.bfloat16).eval()
+    images = smooth_images(frames, 0, dev)
+
+    def forwards(n):
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.no_grad():
+            a.record()
+            for _ in range(n):
+                y, _ = model(images)
+            b.record()
+        torch.cuda.synchronize()
+        return y, a.elapsed_time(b) / n
+
+    res = {}
+    with torch.no_grad():
+        forwards(1)
+        dense_out, dense_ms = forwards(max(1, steps // 2))
+    res["dense"] = {"forward_ms": dense_ms, "frames_per_s": frames / (dense_ms * 1e-3)}
+    log(f"C4 dense: forward {dense_ms:.2f} ms")
+    ref = dense_out.float()
+    for mode in ("vasc", "topk"):
+        alloc = allocation_settings("pi3", mode, 0.75, True)
+        with _ModeEnv("pi3", mode):
+            install.sparse_model_from_pi3(model, sparse_ratio=0.75, layer_sparsity_ratios=alloc["layer_sparsities"],
+                                          verbose=False)
+            forwards(warmup)
+            out, ms = forwards(steps)
+        err = (out.float() - ref).abs()
+        res[mode] = {"forward_ms": ms, "frames_per_s": frames / (ms * 1e-3),
+                     "speedup_vs_dense": dense_ms / ms,
+                     "layer_sparsities": alloc["layer_sparsities"],
+                     "max_abs_diff_vs_dense": float(err.max()), "mean_abs_diff_vs_dense": float(err.mean()),
+                     "dense_output_mean_abs": float(ref.abs().mean())}
+        log(f"C4 {mode}: forward {ms:.2f} ms ({res[mode]['frames_per_s']:.1f} frames/s), vs dense max-abs "
+            f"{res[mode]['max_abs_diff_vs_dense']:.3e} mean-abs {res[mode]['mean_abs_diff_vs_dense']:.3e}")
+        for blk in (model.decoder[i] for i in range(1, len(model.decoder), 2)):  # uninstall: back to dense
+            del blk.attn.forward
+        model._sparse_routing_state = None
+        model._sparse_aux_output_store = None
+    del model, images
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(frames: int, ratio: float, n_layers: int) -> dict:
+    """The reference's CPU-runnable paths restated in torch fp32 on this host's
+    cores: C1 (8 frames, 8328 tokens, H=16) dense and topk, one warm-up then
+    the median of three; one C2 layer (32 frames) dense and topk, single shot.
+    ``value`` scales the C2 topk layer to the 24 global layers' frames/s."""
+    from oracle import cpu_baseline as cb
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    out = {}
+    c1 = [t.float() for t in synthetic_layer(8, 1041, 5, 16, 64, seed=0, device="cpu")]
+    for name, fn in (("topk", lambda: cb.topk_layer(*c1, 0.75)), ("dense", lambda: cb.dense_layer(*c1))):
+        times = []
+        for i in range(4):
+            t0 = time.perf_counter()
+            fn()
+            if i:
+                times.append(time.perf_counter() - t0)
+        out[f"c1_{name}_ms"] = statistics.median(times) * 1e3
+    log(f"cpu baseline: C1 topk {out['c1_topk_ms']:.1f} ms, dense {out['c1_dense_ms']:.1f} ms on {cores} threads")
+    c2 = [t.float() for t in synthetic_layer(frames, 1041, 5, 16, 64, seed=0, device="cpu")]
+    t0 = time.perf_counter()
+    cb.topk_layer(*c2, ratio)
+    topk_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    cb.dense_layer(*c2)
+    dense_s = time.perf_counter() - t0
+    log(f"cpu baseline: C2 layer topk {topk_s:.2f} s, dense {dense_s:.2f} s")
+    out.update({
+        "value": frames / (topk_s * n_layers),
+        "unit": "frames/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"global attention only: one C2 layer (layer 0, s={ratio:.4f}) of the Top-K path (pooled "
+                   f"predictor + top-k + block-gathered attention), torch CPU fp32, single shot, scaled to "
+                   f"{n_layers} layers; beside it the same layer dense and C1 (8 frames) dense/topk as the median "
+                   f"of 3 after a warm-up"),
+        "c2_topk_layer_s": topk_s,
+        "c2_dense_layer_s": dense_s,
+        "c2_dense_frames_per_s": frames / (dense_s * n_layers),
+    })
+    return out
+
+
+def probe_attention(dev) -> int:
+    """Untimed, for rocprofv3 --pmc: five launches of the attention kernel at
+    the C2 shape (q [1,16,33152,64], k/v [1,16,33312,64] bf16 randn; per query
+    block 129 random patch blocks of 518 plus the 3 sink blocks)."""
+    from vasc_amd import ops
+    H, D, Np, Tk = 16, 64, 33152, 33312
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(1, H, Np, D, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, H, Tk, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, H, Tk, D, device=dev, generator=g).to(torch.bfloat16)
+    qb, kb, kbt = 259, 518, 521
+    keys = torch.rand(1, H, qb, kb, device=dev, generator=g)
+    pick = torch.topk(keys, 129, dim=-1).indices
+    sinks = torch.arange(kb, kbt, device=dev).expand(1, H, qb, kbt - kb)
+    index = torch.sort(torch.cat([pick, sinks], -1), -1).values.to(torch.int32).contiguous()
+    count = torch.full((1, H, qb), 132, device=dev, dtype=torch.int32)
+    vt = ops.pack_v(v)
+    for _ in range(5):
+        ops.block_sparse_attn(q, k, vt, index, count)
+    torch.cuda.synchronize()
+    log("attention probe done")
+    return 0
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c2",
+                    help="c2: the metric's configuration (default); c3: 128 frames at s=0.875; c4: the Pi3-shaped "
+                         "decoder at 64 frames; c5: per-kernel microbenchmarks at T = 16k/64k/256k")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sparse-op", action="store_true", help="skip the 24-layer sparse-op step (extras)")
+    ap.add_argument("--no-graph", dest="graph", action="store_false", default=True,
+                    help="time the sparse-op step eagerly only (no HIP graph replay)")
+    ap.add_argument("--probe", choices=("attention", "aggregator", "traffic"),
+                    help="untimed runs for rocprofv3: five C2 attention launches; three C2 vasc aggregator "
+                         "forwards; a 256 MiB copy (counter calibration) then one eager sparse-op step")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the sparse op would shard by head, one head group per GPU). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    from vasc_amd import pipeline
+    from vasc_amd.launcher import layer_sparsity
+
+    dev = torch.device("cuda:0")
+    if args.workload == "c5":
+        return run_c5(dev)
+    if args.probe == "attention":
+        return probe_attention(dev)
+    frames, sparsity = {"c2": (32, 0.75), "c3": (128, 0.875), "c4": (64, 0.75)}[args.workload]
+    ratios = layer_sparsity("vggt", sparsity, "paper") or [sparsity] * 24
+    if args.probe == "aggregator":
+        from vasc_amd import install
+        agg = build_aggregator(dev)
+        g = torch.Generator(device=dev).manual_seed(0)
+        images = torch.rand(1, frames, 3, 392, 518, device=dev, generator=g)
+        with _ModeEnv("vggt", "vasc"), torch.no_grad():
+            install.sparse_aggregator_from_vggt_layerwise(agg, layer_sparsity_ratios=ratios, verbose=False)
+            for _ in range(3):
+                agg(images)
+        torch.cuda.synchronize()
+        log("aggregator probe done")
+        return 0
+    if args.probe == "traffic":
+        layers = [synthetic_layer(frames, 1041, 5, 16, 64, seed=li, device=dev) for li in range(24)]
+        src = torch.empty(128 * 2**20, dtype=torch.bfloat16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # 256 MiB read + 256 MiB written: the FETCH_SIZE / WRITE_SIZE scale
+        run_step(layers, ratios, pipeline.Ledger(), Timer(enabled=False))
+        torch.cuda.synchronize()
+        log("traffic probe done")
+        return 0
+
+    if args.workload == "c4":
+        c4 = run_c4(dev, args.steps, args.warmup)
+        v = c4["vasc"]
+        result = {
+            "metric": "Pi3-shaped decoder forward, vasc @75% sparsity, 64 frames; frames/s",
+            "value": v["frames_per_s"], "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": v["forward_ms"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic: seeded smooth noise (28x37 uniform noise bilinearly upsampled to 392x518)",
+            "config": {"workload": "C4 Pi3-shaped decoder forward (36 blocks, 18 global), vasc and topk vs dense",
+                       "frames": frames, "tokens": frames * 1041, "heads": 16, "head_dim": 64, "dim": 1024,
+                       "sparsity": sparsity, "structural_allocation": True},
+            "c4": c4,
+        }
+        print(json.dumps(result), flush=True)
+        return 0
+
+    N, P, S, H, D, L = frames, 1041, 5, 16, 64, 24
+    agg = run_aggregator(dev, N, ratios, args.steps, args.warmup, dense_reps=3 if args.workload == "c2" else 1)
+    v = agg["vasc"]
+    achieved = agg["attn_flops_per_launch"] / (agg["attn_ms_per_launch"] * 1e-3) / 1e12
+    result = {
+        "metric": METRIC if args.workload == "c2" else
+        f"sparse global-attn layer ms + eff. TFLOP/s @{sparsity:g} sparsity, {N} frames; frames/s",
+        "value": v["frames_per_s"],
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": v["forward_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": f"synthetic: random-init bf16 weights, seeded uniform-noise images [1,{N},3,392,518]",
+        "config": {
+            "workload": f"{args.workload.upper()} VGGT-shaped aggregator forward (24 frame + 24 global blocks, "
+                        f"dim 1024, 16 heads, MLP 4096) with the vasc sparse global attention",
+            "frames": N, "tokens": N * P, "patch_tokens": N * (P - S), "heads": H, "head_dim": D,
+            "global_layers": L, "mode": "vasc", "sparsity": sparsity, "structural_allocation": True,
+        },
+        "global_layer_ms": v["global_layer_ms"],
+        "frames_per_s_global_layers": v["frames_per_s_global_layers"],
+        "speedup_global_layer_vs_dense": agg["speedup_global_layers_vs_dense"],
+        "aggregator": agg,
+        "roofline": {
+            "kernel": "bsattn_fwd_kernel (vasc_global_attn_fwd: patch queries over their lists + special queries)",
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / PEAK_BF16_TFLOPS,
+            "traffic": traffic_bytes() if args.workload == "c2" else None,
+            "traffic_source": TRAFFIC_SUMMARY if args.workload == "c2" else None,
+            "flops_per_launch": agg["attn_flops_per_launch"],
+            "ms_per_launch": agg["attn_ms_per_launch"],
+            "launches_timed": agg["attn_launches"],
+        },
+    }
+    if not args.no_sparse_op:
+        result["sparse_op"] = run_sparse_op(dev, N, ratios, args.steps, args.warmup, args.graph, dense=True)
+    if not args.no_cpu_baseline and args.workload == "c2":
+        result["cpu_baseline"] = cpu_baseline(N, ratios[0], L)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -131,6 +131,18 @@ def test_cpu_baseline_matches_float64_oracle():
     np.testing.assert_allclose(out.numpy(), ref, atol=2e-5)
 
 
+def test_cpu_dense_baseline_matches_float64_oracle():
+    g = torch.Generator().manual_seed(6)
+    Np, Tk, H, D = 300, 333, 2, 64
+    q = torch.randn(1, H, Np, D, generator=g)
+    k = torch.randn(1, H, Tk, D, generator=g)
+    v = torch.randn(1, H, Tk, D, generator=g)
+    out = CB.dense_layer(q, k, v, rows=128)  # several row chunks, a partial last one
+    idx, cnt = OA.dense_lists(1, H, Np, Tk)
+    ref = OA.block_sparse_attention(q.double().numpy(), k.double().numpy(), v.double().numpy(), idx, cnt)
+    np.testing.assert_allclose(out.numpy(), ref, atol=2e-5)
+
+
 # ---------------------------------------------------------------- PV post-cut
 def _rank_one(levels, Nq=128, block_k=64, a=1.0):
     """q rows = a * e0, key block j = levels[j] * e0: every logit of block j
