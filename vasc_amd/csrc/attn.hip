@@ -28,9 +28,16 @@
 //  * K and Vt tiles arrive by LDS DMA (global_load_lds_dwordx4) into a
 //    double-buffered LDS tile one block ahead of the MFMAs, with a
 //    16-byte-chunk xor swizzle ((row/2)%8) that spreads the rows an MFMA
-//    operand read touches over all LDS banks. The DMA is issued through asm:
-//    the compiler cannot tell a DMA into the other buffer from one into the
-//    buffer being read and would drain it before every LDS read.
+//    operand read touches over all LDS banks. The DMA is issued through asm
+//    without a memory clobber (the explicit waits and barriers order it), so
+//    the compiler neither drains it before LDS reads nor turns the uniform
+//    list reads into vector loads: the lists are read through the constant
+//    address space on the scalar unit, and nothing but the DMA counts in
+//    vmcnt inside the loop. Q is consumed before the loop so that its load
+//    wait stays out of the loop body.
+//  * The loop body runs two blocks per trip (buffers 0 and 1), so every LDS
+//    operand address is a lane constant plus an immediate offset; all eight K
+//    (and Vt) operand reads of a block are issued before its first product.
 //  * workgroup ids are remapped so each XCD walks a contiguous range of
 //    query blocks of the same head (K/V reuse in that XCD's L2).
 //  * vasc_global_attn_fwd adds the layer's special-token queries, which
@@ -97,6 +104,16 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 constexpr float kHigh = 18446744073709551616.0f;  // 2^64
 constexpr float kLow = 8.673617379884035e-19f;    // 2^-60
 
+// LDS DMA without a memory clobber (the waits and barriers that order it are
+// explicit); uniform list reads then stay on the scalar unit.
+__device__ __forceinline__ void dma16(const void *sbase, uint32_t voff_bytes, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voff_bytes), "s"(sbase));
+}
+
 template <bool kDense, bool kPv = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void bsattn_fwd_kernel(const AttnParams p) {
@@ -155,6 +172,9 @@ void bsattn_fwd_kernel(const AttnParams p) {
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       qf[s] = qvalid ? *reinterpret_cast<const u32x4 *>(qptr + 16 * s + 8 * hf) : u32x4{0, 0, 0, 0};
+    // consume Q here so that the compiler's wait for these loads lands before
+    // the loop instead of inside it
+    asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]));
   }
 
   // Staging: LDS chunk ci = u*256 + tid lands at byte 16*ci (the DMA writes
@@ -165,31 +185,35 @@ void bsattn_fwd_kernel(const AttnParams p) {
   const int nk32 = static_cast<int>(p.nk);
   const int nkb32 = static_cast<int>(p.nkb);
   const int partial = (nk32 % kBlockK) ? nkb32 - 1 : -1;  // the partial last block, if any
-  uint32_t koffb[CH], koffl[CH], voffb[CH];                 // per-lane byte offsets in a block
-#pragma unroll
-  for (int u = 0; u < CH; ++u) {
-    const int ci = u * kThreads + tid;
-    const int r = ci >> 3, c = (ci & 7) ^ swz(r);
-    koffb[u] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_st + c * 8) * 2);
-    voffb[u] = static_cast<uint32_t>((r * kHeadDim + c * 8) * 2);
-    // rows of the partial block past the sequence end read the last row
-    const int t = partial * kBlockK + r;
-    koffl[u] = (partial < 0 || t < nk32)
-                   ? koffb[u]
-                   : static_cast<uint32_t>(koffb[u] + static_cast<int64_t>(nk32 - 1 - t) * p.k_st * 2);
-  }
+  // swz(32u + r) = swz(r): a thread's chunk column, and so its byte offset
+  // inside the block, is the same for each of its CH chunks; only the row
+  // base (32u rows) moves, and that goes into the scalar base address.
+  const int r0 = tid >> 3;
+  const int cc = (tid & 7) ^ swz(r0);
+  const uint32_t koff = static_cast<uint32_t>((static_cast<int64_t>(r0) * p.k_st + cc * 8) * 2);
+  const uint32_t voff = static_cast<uint32_t>((r0 * kHeadDim + cc * 8) * 2);
+  const int last_row = partial >= 0 ? nk32 - 1 - partial * kBlockK : kBlockK - 1;
   // K and Vt of block blk -> LDS buffer buf. Blocks outside [0, nkb) load
-  // block 0 (their scores are masked).
+  // block 0 (their scores are masked); rows of the partial block past the
+  // sequence end read its last row.
   auto fetch = [&](int blk, int buf) {
     const int sb = (blk >= 0 && blk < nkb32) ? blk : 0;
     const uint16_t *kb = kbase + static_cast<int64_t>(sb) * kBlockK * p.k_st;
     const uint16_t *vb = vbase + static_cast<int64_t>(sb) * kTile;
     const uint32_t kd = lds_u32(smem[buf][0]) + w * 64 * 16, vd = lds_u32(smem[buf][1]) + w * 64 * 16;
+    if (sb == partial) {
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      lds_dma16(kb, sb == partial ? koffl[u] : koffb[u], kd + u * kThreads * 16);
-      lds_dma16(vb, voffb[u], vd + u * kThreads * 16);
+      for (int u = 0; u < CH; ++u) {
+        const int r = 32 * u + r0;
+        const int rr = r < last_row ? r : last_row;
+        dma16(kb, static_cast<uint32_t>((static_cast<int64_t>(rr) * p.k_st + cc * 8) * 2), kd + u * kThreads * 16);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < CH; ++u) dma16(kb + 32 * u * p.k_st, koff, kd + u * kThreads * 16);
     }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) dma16(vb + 32 * u * kHeadDim, voff, vd + u * kThreads * 16);
   };
   // Keys of block blk that exist: 64, fewer for the partial last block, 0
   // for blocks outside [0, nkb).
@@ -270,21 +294,24 @@ void bsattn_fwd_kernel(const AttnParams p) {
   // List entry j+1 is loaded during iteration j-1 (index clamped to the list)
   // so that reading it never waits on memory: the wait at the top of each
   // iteration already covers it.
-  int blk = dense ? 0 : __builtin_amdgcn_readfirstlane(list[0]);
-  int32_t e_next = dense ? 0 : list[n > 1 ? 1 : 0];
+  const __attribute__((address_space(4))) int32_t *clist =
+      (const __attribute__((address_space(4))) int32_t *)(list);
+  int blk = dense ? 0 : clist[0];
+  int32_t e_next = dense ? 0 : clist[n > 1 ? 1 : 0];
   fetch(blk, 0);
-  for (int j = 0; j < n; ++j) {
-    const int buf = j & 1;
-    // Block j landed (every wave's share), and every wave is done with buffer buf^1.
+  // One block: wait for its tiles, start the next block's DMA into the other
+  // buffer, compute. The loop runs two blocks per trip so that each block's
+  // buffer, and with it every LDS address, is a compile-time constant.
+  auto step = [&](const int j, const int buf) {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     const int cur = blk;
     if (j + 1 < n) {
       if (dense) {
         blk = j + 1;
       } else {
-        const int e = __builtin_amdgcn_readfirstlane(e_next);
+        const int e = e_next;
         blk = p.delta ? blk + e : e;
-        e_next = list[j + 2 < n ? j + 2 : n - 1];
+        e_next = clist[j + 2 < n ? j + 2 : n - 1];
       }
       fetch(blk, buf ^ 1);
     }
@@ -293,14 +320,21 @@ void bsattn_fwd_kernel(const AttnParams p) {
 
     // S^T tiles: keys 32t + [0,32) x this wave's 32 query rows.
     floatx16 S[2];
+    u32x4 ka[4][2];  // all K operands of the block, read before the first product
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int row = 32 * t + lr;
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(ks + row * kHeadDim + ((2 * s + hf) ^ swz(row)) * 8);
-        S[t] = mfma32(a, qf[s], s == 0 ? zero16 : S[t]);
+        ka[s][t] = *reinterpret_cast<const u32x4 *>(ks + row * kHeadDim + ((2 * s + hf) ^ swz(row)) * 8);
       }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) S[t] = mfma32(ka[s][t], qf[s], s == 0 ? zero16 : S[t]);
+    // every K read issued before the first score product
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
 
     // PV post-cut (qk_int_sv_f16_cuda_sm80.cuh:291-381 with update_mo,
     // attn_utils.cuh:419-466, per-block mode): gap = the largest over the
@@ -335,7 +369,7 @@ void bsattn_fwd_kernel(const AttnParams p) {
         // barrier wait overlaps them
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const float g4 = fmaxf(fmaxf(pv_gap[0], pv_gap[1]), fmaxf(pv_gap[2], pv_gap[3]));
-        if (!(g4 + pv_threshold > 0.f)) continue;  // skipped: no sum, no PV
+        if (!(g4 + pv_threshold > 0.f)) return;  // skipped: no sum, no PV
         if (l == 0 && p.pv_map && cur >= 0 && cur < nkb32)
           p.pv_map[((bh * p.nqb + qb) * 4 + w) * p.pv_w + cur] = 1;
       }
@@ -344,14 +378,25 @@ void bsattn_fwd_kernel(const AttnParams p) {
     if (__ballot(!(bs <= kHigh) || !(ls + bs >= kLow)) || lim < kBlockK) bs = slow(S, pb, lim);
     ls += bs;
 
+    u32x4 va[4][2];  // all Vt operands of the block, read before the first product
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) {
         const int row = 32 * n2 + lr;
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(vs + row * kHeadDim + ((2 * s + hf) ^ swz(row)) * 8);
-        oacc[n2] = mfma32(a, pb[s], oacc[n2]);
+        va[s][n2] = *reinterpret_cast<const u32x4 *>(vs + row * kHeadDim + ((2 * s + hf) ^ swz(row)) * 8);
       }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int n2 = 0; n2 < 2; ++n2) oacc[n2] = mfma32(va[s][n2], pb[s], oacc[n2]);
+    // every Vt read issued before the first PV product
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  };
+  for (int j = 0; j < n; j += 2) {
+    step(j, 0);
+    if (j + 1 < n) step(j + 1, 1);
   }
 
   const float ltot = ls + __shfl_xor(ls, 32);
