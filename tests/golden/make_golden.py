@@ -13,7 +13,11 @@ does, and run on the CPU; only their inputs and outputs are saved:
   unit-temperature scores, where the ledger accrues debt and the gate both
   opens and closes;
 * ``predict.npz``         ``predict_attention`` on bf16 inputs under CPU bf16
-  autocast (ragged token counts).
+  autocast (ragged token counts);
+* ``selector_scale.npz``  the at-scale chains of ``scale_cases.py`` (C1 with
+  all 16 heads over 6 layers, the C2 block shape over 3 layers): only the
+  reference's outputs (bit-packed selections and the ledger per layer) and a
+  digest of the inputs, which the test regenerates.
 
 Usage: ``python tests/golden/make_golden.py [/root/reference]``.
 """
@@ -141,6 +145,25 @@ def main(ref_root: Path) -> None:
         out[f"prob{i}"] = prob.float().numpy()
         out[f"prob_dtype{i}"] = np.array(str(prob.dtype))
     np.savez_compressed(OUT / "predict.npz", **out)
+
+    # 4. at-scale chains (inputs regenerated by the test from scale_cases.py)
+    sys.path.insert(0, str(OUT))
+    import scale_cases
+    scale = {}
+    for case in scale_cases.CASES:
+        state = {}
+        hashes = []
+        for layer, scores, values, capacity, protected, hint in scale_cases.layer_inputs(case):
+            selected = fn(scores, values, torch.arange(scores.shape[-1]).view(1, 1, 1, -1) < capacity,
+                          layer_idx=layer, routing_state=state, protected_mask=protected, fp32_projection=True,
+                          max_capacity_hint=hint)
+            hashes.append(scale_cases.digest(_np(scores), _np(values), _np(capacity), _np(protected)))
+            scale[f"{case}_l{layer}_selected"] = np.packbits(_np(selected).astype(bool), axis=-1)
+            scale[f"{case}_l{layer}_debt"] = _np(state["cosa_value_risk_pair_debt"])
+            scale[f"{case}_l{layer}_arrival"] = _np(state["cosa_value_risk_pair_pending_arrival"])
+            scale[f"{case}_l{layer}_service"] = _np(state["qk_pv_service_observation"]["pair_service_fraction"])
+        scale[f"{case}_digest"] = np.array(scale_cases.digest(np.array(hashes)))
+    np.savez_compressed(OUT / "selector_scale.npz", **scale)
     print("wrote", sorted(p.name for p in OUT.glob("*.npz")))
 
 

@@ -120,3 +120,63 @@ def test_predict_attention_goldens_bit_exact_after_bf16():
         wrong, _, _ = OP.pooled_prob(q, k, bf16=False)
         loose += int(not np.array_equal(OP.bf16_round(wrong), ref))
     assert loose >= 1  # dropping the bf16 logit rounding is detected
+
+
+def test_selector_at_scale_matches_reference_outside_near_ties():
+    """The reference's selector at config 1 (all 16 heads, 6 layers) and
+    config 2 (16 x 259 x 518 blocks, 3 layers) block shapes, teacher-forced
+    per layer. Every row whose oracle priority has a relative gap above 1e-5
+    between the last kept and the first dropped block (the reference's fp32
+    reduction order moves priorities by about 2e-6) selects exactly the
+    reference's blocks; rows inside that margin are counted and reported.
+    The C1 chain takes the debt priority (the gate opens in layers 1, 3, 4
+    and 5); the C2 chain accrues and settles debt at full size."""
+    import sys
+    sys.path.insert(0, str(GOLDEN))
+    import scale_cases
+
+    g = _load("selector_scale.npz")
+    report = {}
+    for case, cfg in scale_cases.CASES.items():
+        layers = [tuple(t.numpy() if hasattr(t, "numpy") else t for t in item)
+                  for item in scale_cases.layer_inputs(case)]
+        hashes = [scale_cases.digest(s, v, c, p) for _, s, v, c, p, _ in layers]
+        assert scale_cases.digest(np.array(hashes)) == str(g[f"{case}_digest"]), \
+            "regenerated inputs differ from the fixture's (torch's CPU generator changed?)"
+        K = cfg["K"]
+        near = near_diff = rows = 0
+        for layer, s, v, cap, prot, hint in layers:
+            st = {} if layer == 0 else {
+                OS.STATE_KEY: g[f"{case}_l{layer - 1}_debt"],
+                OS.PENDING_KEY: g[f"{case}_l{layer - 1}_arrival"],
+                OS.PENDING_LAYER_KEY: layer - 1,
+                OS.SERVICE_KEY: {"layer_idx": layer - 1, "identity_observed": True,
+                                 "pair_service_fraction": g[f"{case}_l{layer - 1}_service"]},
+            }
+            sel, info = OS.cosa_select(s, v, cap[..., 0], layer_idx=layer, state=st,
+                                       protected=prot if prot.any() else None, max_capacity_hint=hint)
+            ref = np.unpackbits(g[f"{case}_l{layer}_selected"], axis=-1, count=K).astype(bool)
+            prio, count = info["priority"], info["count"]
+            srt = -np.sort(-prio, axis=-1)
+            c = np.clip(count, 1, K)[..., None]
+            upper = np.take_along_axis(srt, c - 1, -1)[..., 0]
+            lower = np.take_along_axis(srt, np.minimum(c, K - 1), -1)[..., 0]
+            gap = np.where(count < K, upper - lower, np.inf)
+            decided = gap > 1e-5 * np.maximum(np.abs(upper), 1e-30)
+            differ = (sel != ref).any(-1)
+            assert not (differ & decided).any(), f"{case} layer {layer}: a decided row differs from the reference"
+            assert (sel.sum(-1) == ref.sum(-1)).all()
+            near += int((~decided).sum())
+            near_diff += int((differ & ~decided).sum())
+            rows += decided.size
+            np.testing.assert_allclose(info["debt"].reshape(-1), g[f"{case}_l{layer}_debt"].reshape(-1),
+                                       rtol=2e-6, atol=1e-9)
+            np.testing.assert_allclose(info["arrival"].reshape(-1), g[f"{case}_l{layer}_arrival"].reshape(-1),
+                                       rtol=2e-6, atol=1e-9)
+        report[case] = (rows, near, near_diff)
+        if case == "c2":
+            assert (g["c2_l2_debt"] > 0).mean() > 0.05  # the ledger carries debt at this size
+        print(f"{case}: {rows} rows, {near} within the near-tie margin, {near_diff} of them select differently")
+    # the margin excludes only a small share of rows
+    for case, (rows, near, _) in report.items():
+        assert near <= 0.02 * rows, (case, near, rows)
