@@ -115,6 +115,19 @@ int vasc_pair_innovation(const float *pooled_v, int64_t B, int64_t H,
 size_t vasc_select_workspace_size(int64_t B, int64_t H, int64_t q_blocks,
                                   int64_t k_blocks);
 
+/* Regions of the VASC selection workspace that hold per-call results after
+ * a VASC_MODE_VASC call (read back for the reference's routing statistics,
+ * sparse_wrapper.py:4032-4096): */
+#define VASC_WS_ROW_TOTAL 0     /* [B,H,Q] f32: sum_k score*innovation (risk total) */
+#define VASC_WS_ROW_PAIR_SUM 1  /* [B,H,Q] f32: sum_p of the row's pair arrival   */
+#define VASC_WS_ROW_CAPACITY 2  /* [B,H,Q] i32: the row's QK capacity             */
+#define VASC_WS_ADMITTED_DEBT 3 /* [B,H,P] f32: admitted debt per pair            */
+
+/* Byte offset of a region inside the workspace for these sizes; -1 for an
+ * unknown region or empty sizes. Host-only. */
+int64_t vasc_select_workspace_offset(int64_t B, int64_t H, int64_t q_blocks,
+                                     int64_t k_blocks, int32_t region);
+
 /*
  * Kernel 2: per-row block selection writing ascending index lists.
  *

@@ -101,3 +101,21 @@ def pooled_prob(q: np.ndarray, k: np.ndarray, ks_q: int = 128, ks_k: int = 64, *
         pq = pool_blocks(q, ks_q, round_bf16=bf16)
         pk = pool_blocks(k, ks_k, round_bf16=bf16)
     return softmax(pooled_logits(pq, pk, bf16=bf16)), pq, pk
+
+
+def key_block_variance(k: np.ndarray, ks_k: int = 64, *, bf16: bool = True) -> np.ndarray:
+    """``predict_attention(..., return_key_block_variance=True)``'s second
+    output (ATT:69-89): per 64-key block, the mean over its real tokens of
+    the squared token norm minus the squared norm of the block mean, clamped
+    at 0, ``[B,H,Kb]`` float32. With ``bf16`` the token squares are rounded to
+    bfloat16 before their float32 sum (``key * key`` on bf16 keys) and the
+    block mean is the bf16-rounded mean, as under bf16 autocast."""
+    k = np.asarray(k, np.float32)
+    sq = (k * k).astype(np.float32)
+    if bf16:
+        sq = bf16_round(sq)
+    tok = sq.astype(np.float64).sum(-1).astype(np.float32)                  # [B,H,T]
+    mean_sq = pool_blocks(tok[..., None], ks_k)[..., 0]                      # float32 block means
+    mean = pool_blocks(k, ks_k, round_bf16=bf16)                             # [B,H,Kb,D]
+    sq_mean = (mean.astype(np.float64) ** 2).sum(-1).astype(np.float32)
+    return np.maximum((mean_sq - sq_mean).astype(np.float32), np.float32(0.0))

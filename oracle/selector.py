@@ -382,8 +382,64 @@ def cosa_select(score, pooled_value, cap, *, layer_idx: int, state: dict,
     info = dict(arrival=arrival, pair_cap=pair_cap, row_arrival=A, row_pair=a,
                 rowpair=rowpair, total=total, gate=gate, admitted=adm,
                 debt_before=debt_before, debt=debt, reflection=refl,
-                service=service, priority=prio, iota=iota, count=count, M=M)
+                service=service, priority=prio, iota=iota, count=count, M=M,
+                settled=np.zeros_like(debt) if pending is None else np.asarray(pending, np.float32).reshape(B, H, P),
+                consumed=service_prev, selected=selected)
     return selected, info
+
+
+def routing_stats(info: dict, cap, base_mask, protected=None, counterfactual: bool = True) -> dict:
+    """The selector's routing statistics (SW:4032-4096) from a ``cosa_select``
+    call's ``info`` (float64 means of the float32 quantities): ledger flow of
+    the settlement, gate, capacity, QK overlap with ``base_mask`` (bool
+    ``[B,H,Q,K]``), budget and conservation errors and, with
+    ``counterfactual``, the overlap of the current-only (row arrival) and the
+    debt (arrival + admitted debt) selections."""
+    debt_before = np.asarray(info["debt_before"], np.float32)
+    settled = np.asarray(info.get("settled", np.zeros_like(debt_before)), np.float32)
+    consumed = np.asarray(info.get("consumed", np.zeros_like(debt_before)), np.float32)
+    refl = np.asarray(info["reflection"], np.float32)
+    debt = np.asarray(info["debt"], np.float32)
+    useful = float(clamp_min0((consumed - refl).astype(np.float32)).astype(np.float64).sum())
+    wasted = float(refl.astype(np.float64).sum())
+    total = float(consumed.astype(np.float64).sum())
+    cap = np.asarray(cap, np.int64)
+    selected = info["selected"]
+    denom = np.maximum(cap, 1).astype(np.float64)
+    overlap = (selected & np.asarray(base_mask, bool)).sum(-1)
+    out = {
+        "cosa_pair_debt_enabled": 1.0,
+        "cosa_pair_service_useful_repayment": useful,
+        "cosa_pair_service_wasted": wasted,
+        "cosa_pair_service_utilization": useful / max(total, 1e-8) if total > 0 else 0.0,
+        "cosa_pair_service_gate_debt": float(info["gate"]),
+        "cosa_pair_qk_capacity": float(cap.mean()),
+        "cosa_pair_arrival": float(np.asarray(info["arrival"], np.float64).sum(-1).mean()),
+        "cosa_pair_innovation": float(np.asarray(info["iota"], np.float64).mean()),
+        "cosa_pair_debt_before_service": float(debt_before.astype(np.float64).mean()),
+        "cosa_pair_settled_arrival": float(settled.astype(np.float64).sum(-1).mean()),
+        "cosa_pair_consumed_pv_service": float(consumed.astype(np.float64).sum(-1).mean()),
+        "cosa_pair_admitted_debt": float(np.asarray(info["admitted"], np.float64).sum(-1).mean()),
+        "cosa_pair_backlog": float(debt.astype(np.float64).sum(-1).mean()),
+        "cosa_pair_qk_overlap": float((overlap / denom).mean()),
+        "cosa_pair_qk_swap_fraction": float((1.0 - overlap / denom).mean()),
+        "cosa_pair_budget_error": float(np.abs(selected.sum(-1) - cap).max()),
+        "cosa_pair_conservation_error": float(np.abs(
+            debt.astype(np.float64) - debt_before - settled + consumed - refl).max()),
+    }
+    if counterfactual:
+        A = np.asarray(info["row_arrival"], np.float32)
+        K = A.shape[-1]
+        adm_k = np.repeat(np.asarray(info["admitted"], np.float32), 2, axis=-1)[..., :K]
+        cur_p, debt_p = A, (A + adm_k[..., None, :]).astype(np.float32)
+        if protected is not None:
+            cur_p = np.where(protected, FLT_MAX, cur_p).astype(np.float32)
+            debt_p = np.where(protected, FLT_MAX, debt_p).astype(np.float32)
+        count = info["count"]
+        both = (select_top(cur_p, count) & select_top(debt_p, count)).sum(-1)
+        out["cosa_pair_current_debt_overlap"] = float((both / denom).mean())
+        out["cosa_pair_history_swap_fraction"] = float((1.0 - both / denom).mean())
+    return out
 
 
 def finalize(state: dict) -> dict:
@@ -414,6 +470,8 @@ def finalize(state: dict) -> dict:
         "cosa_pair_terminal_arrival": float(pending.sum(-1).mean()),
         "cosa_pair_terminal_service": float(service.sum(-1).mean()),
         "cosa_pair_terminal_backlog": float(terminal.sum(-1).mean()),
+        "cosa_pair_terminal_conservation_error": float(np.abs(
+            terminal.astype(np.float64) - prev - pending + service - refl).max()),
     }
 
 

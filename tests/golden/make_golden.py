@@ -57,11 +57,14 @@ def _np(t):
     return t.detach().cpu().numpy()
 
 
-def selector_chain(fn, rng_torch, K, Q, H, layers, protect_last, *, capacity_fn, hint=None, peak=1.0):
-    """Run one routing_state chain; return per-layer arrays."""
+def selector_chain(fn, rng_torch, K, Q, H, layers, protect_last, *, capacity_fn, hint=None, peak=1.0,
+                   stats=False):
+    """Run one routing_state chain; return per-layer arrays (with ``stats``
+    also the selector's routing statistics per layer, ``stat_<key>``)."""
     state = {}
     rec = {k: [] for k in ("score", "value", "cap", "protected", "selected", "priority", "debt", "arrival",
                            "service", "indices")}
+    stat_rec: dict = {}
     for layer in range(layers):
         scores = (torch.randn(1, H, Q, K, generator=rng_torch) * peak).softmax(-1)
         values = torch.randn(1, H, K, 13, generator=rng_torch)
@@ -70,8 +73,11 @@ def selector_chain(fn, rng_torch, K, Q, H, layers, protect_last, *, capacity_fn,
         protected = torch.zeros_like(base)
         if protect_last:
             protected[..., -1:] = capacity > 0
+        store = {} if stats else None
         selected = fn(scores, values, base, layer_idx=layer, routing_state=state, protected_mask=protected,
-                      fp32_projection=True, max_capacity_hint=hint)
+                      fp32_projection=True, max_capacity_hint=hint, stats_store=store)
+        for key, val in (store or {}).items():
+            stat_rec.setdefault(f"stat_{key}", []).append(_np(val))
         rec["score"].append(_np(scores))
         rec["value"].append(_np(values))
         rec["cap"].append(_np(capacity[..., 0]))
@@ -83,7 +89,9 @@ def selector_chain(fn, rng_torch, K, Q, H, layers, protect_last, *, capacity_fn,
         rec["service"].append(_np(state["qk_pv_service_observation"]["pair_service_fraction"]))
         idx = _np(state["cosa_value_risk_pair_selected_indices"])
         rec["indices"].append(idx)
-    return {k: np.stack(v) for k, v in rec.items() if k != "indices"}, state
+    out = {k: np.stack(v) for k, v in rec.items() if k != "indices"}
+    out.update({k: np.stack(v) for k, v in stat_rec.items()})
+    return out, state
 
 
 def main(ref_root: Path) -> None:
@@ -123,9 +131,16 @@ def main(ref_root: Path) -> None:
         base[..., K - 1] = True
         return base.sum(-1, keepdim=True)
 
-    rec, state = selector_chain(fn, gen, K, Q, H, 6, True, capacity_fn=c1_capacity, hint=topk + 1, peak=1.0)
-    fin(state)
+    # routing statistics with the reference's default counterfactual statistics on
+    os.environ["SPARSE_VGGT_COSA_COUNTERFACTUAL_STATS"] = "1"
+    rec, state = selector_chain(fn, gen, K, Q, H, 6, True, capacity_fn=c1_capacity, hint=topk + 1, peak=1.0,
+                                stats=True)
+    os.environ["SPARSE_VGGT_COSA_COUNTERFACTUAL_STATS"] = RELEASE_SWITCHES["COUNTERFACTUAL_STATS"]
+    terminal = {}
+    fin(state, stats_store=terminal)
     rec["terminal_debt"] = _np(state["cosa_value_risk_pair_debt"])
+    for key, val in terminal.items():
+        rec[f"terminal_stat_{key}"] = _np(val)
     np.savez_compressed(OUT / "selector_c1.npz", **rec)
 
     # 3. predict_attention under CPU bf16 autocast
@@ -140,6 +155,10 @@ def main(ref_root: Path) -> None:
         k = (torch.randn(1, 2, nk, 64, generator=g) * 2).to(torch.bfloat16)
         with torch.autocast("cpu", dtype=torch.bfloat16):
             prob = pa(q, k)
+            _, var = pa(q, k, return_key_block_variance=True)
+            _, var_max = pa(q, k, pool_mode="max", return_key_block_variance=True)
+        out[f"var{i}"] = var.float().numpy()
+        out[f"var_max{i}"] = var_max.float().numpy()
         out[f"q{i}"] = q.float().numpy()
         out[f"k{i}"] = k.float().numpy()
         out[f"prob{i}"] = prob.float().numpy()

@@ -180,3 +180,54 @@ def test_selector_at_scale_matches_reference_outside_near_ties():
     # the margin excludes only a small share of rows
     for case, (rows, near, _) in report.items():
         assert near <= 0.02 * rows, (case, near, rows)
+
+
+def test_routing_stats_match_reference_goldens():
+    """The selector's routing statistics (SW:4032-4096, counterfactual
+    statistics on) and the terminal settlement statistics (SW:4158-4175),
+    written by the reference for every layer of the C1 chain, against the
+    oracle's restatement on the teacher-forced replay."""
+    g = _load("selector_c1.npz")
+    rec = {k: g[k] for k in g.files}
+    keys = [k[len("stat_"):] for k in rec if k.startswith("stat_")]
+    assert len(keys) == 19
+    K = rec["score"].shape[-1]
+    for l in range(rec["score"].shape[0]):
+        st = {} if l == 0 else _state_from(rec, l)
+        prot = rec["protected"][l].astype(bool)
+        cap = rec["cap"][l]
+        _, info = OS.cosa_select(rec["score"][l], rec["value"][l], cap, layer_idx=l, state=st,
+                                 protected=prot if prot.any() else None, max_capacity_hint=int(130 * 0.25) + 1)
+        base = np.arange(K).reshape(1, 1, 1, K) < cap[..., None]
+        ours = OS.routing_stats(info, cap, base, protected=prot if prot.any() else None)
+        assert set(ours) == set(keys)
+        for key in keys:
+            ref = float(rec[f"stat_{key}"][l])
+            swap = "overlap" in key or "swap" in key
+            np.testing.assert_allclose(ours[key], ref, rtol=1e-5, atol=2e-3 if swap else 1e-6,
+                                       err_msg=f"layer {l} {key}")
+    # terminal settlement of the last layer
+    st = _state_from(rec, rec["score"].shape[0])
+    out = OS.finalize(st)
+    for key in (k for k in rec if k.startswith("terminal_stat_")):
+        np.testing.assert_allclose(float(out[key[len("terminal_stat_"):]]), float(rec[key]), rtol=1e-5, atol=1e-7,
+                                   err_msg=key)
+
+
+def test_key_block_variance_goldens():
+    """predict_attention(return_key_block_variance=True)'s variance proxy
+    (ATT:69-89) from the reference under CPU bf16 autocast, avg and max
+    pooling (the latter takes the mean from avg_pool1d too): the oracle agrees
+    to float32 summation order; dropping the bf16 rounding of the token
+    squares is detected."""
+    g = _load("predict.npz")
+    n = len([f for f in g.files if f.startswith("var") and not f.startswith("var_max")])
+    assert n == 3
+    loose = 0
+    for i in range(n):
+        ours = OP.key_block_variance(g[f"k{i}"])
+        for ref in (g[f"var{i}"], g[f"var_max{i}"]):
+            np.testing.assert_allclose(ours, ref, rtol=2e-6, atol=1e-5)
+        loose += int(np.abs(OP.key_block_variance(g[f"k{i}"], bf16=False) - g[f"var{i}"]).max() > 1e-3)
+    assert loose == n
+

@@ -349,3 +349,98 @@ def test_global_layer_forward_dense_limit():
         ref = m.proj(ref.transpose(1, 2).reshape(1, N * P, dim).to(torch.bfloat16))
     err = (out.float() - ref.float()).abs()
     assert err.max() < 6e-2 and err.mean() < 6e-3, (err.max().item(), err.mean().item())
+
+
+def _check_stats(got, ref, where):
+    assert set(got) >= set(ref), (where, sorted(set(ref) - set(got)))
+    for key, val in ref.items():
+        swap = "overlap" in key or "swap" in key
+        np.testing.assert_allclose(float(got[key]), val, rtol=1e-5, atol=1e-3 if swap else 1e-6,
+                                   err_msg=f"{where} {key}")
+
+
+def test_routing_stats_match_oracle(release_env):
+    """stats_store of get_cosa_value_risk_pair_debt_mask (the reference's 19
+    keys with counterfactual statistics on) and of finalize (6 terminal keys)
+    on a 6-layer chain where debt accrues, against the oracle's routing_stats
+    (pinned to the reference's own statistics by tests/test_golden.py)."""
+    from vasc_amd import sparse_wrapper as SW
+    release_env("pi3", "vasc")
+    rng = np.random.default_rng(13)
+    st_gpu, st_ref = {}, {}
+    B, H, Q, K = 1, 2, 65, 130
+    gates = []
+    for layer in range(6):
+        s = _softmax_rows(rng, (B, H, Q, K))
+        pv = rng.standard_normal((B, H, K, 64)).astype(np.float32)
+        order = np.argsort(-s, axis=-1, kind="stable")
+        base = np.zeros((B, H, Q, K), bool)
+        np.put_along_axis(base, order[..., :32], True, axis=-1)
+        base[..., -1] = True
+        prot = np.zeros_like(base)
+        prot[..., -1] = True
+        cap = base.sum(-1)
+        store = {}
+        SW.get_cosa_value_risk_pair_debt_mask(
+            torch.from_numpy(s).cuda(), torch.from_numpy(pv).cuda(), torch.from_numpy(base).cuda(),
+            layer_idx=layer, routing_state=st_gpu, protected_mask=torch.from_numpy(prot).cuda(),
+            max_capacity_hint=33, stats_store=store)
+        _, info = OS.cosa_select(s, pv, cap, layer_idx=layer, state=st_ref, protected=prot, max_capacity_hint=33)
+        gates.append(bool(info["gate"]))
+        assert len(store) == 19
+        _check_stats(store, OS.routing_stats(info, cap, base, protected=prot), f"layer {layer}")
+    assert any(gates) and (np.asarray(st_ref[OS.STATE_KEY]) > 0).any()
+    term = {}
+    SW.finalize_cosa_value_risk_pair_debt(st_gpu, stats_store=term)
+    assert len(term) == 6
+    _check_stats(term, OS.finalize(st_ref), "terminal")
+
+
+def test_layer_routing_stats_store(release_env):
+    """block_sparse_attn_cuda with a routing_stats_store in vasc mode (the
+    reference passes its base map to the selector and records the resolved
+    PV threshold): the selector's statistics equal the oracle's for the same
+    layer selection."""
+    from vasc_amd.attention import predict_attention
+    from vasc_amd.sparse_wrapper import block_sparse_attn_cuda
+    release_env("pi3", "vasc")
+    torch.manual_seed(4)
+    N, P, S = 2, 1041, 5
+    n_patch, n_total = N * (P - S), N * P
+    state, st_ref = {}, {}
+    for layer in range(3):
+        q = torch.randn(1, 2, n_patch, 64, device="cuda").to(torch.bfloat16)
+        k, v = (torch.randn(1, 2, n_total, 64, device="cuda").to(torch.bfloat16) for _ in range(2))
+        score = predict_attention(q, k[:, :, :n_patch])
+        store = {}
+        block_sparse_attn_cuda(q, k, v, score, sparse_ratio=0.75, num_patch_tokens=n_patch, layer_idx=layer,
+                               routing_state=state, routing_stats_store=store)
+        from vasc_amd import ops
+        iota = ops.pool_qkv(v=v[:, :, :n_patch])[3].cpu().numpy()
+        sc = score.cpu().numpy()
+        Kb = sc.shape[-1]
+        final, info = OS.layer_selection(sc, mode="vasc", sparse_ratio=0.75, patch_tokens=n_patch,
+                                         total_tokens=n_total, official_mask=False, state=st_ref, layer_idx=layer,
+                                         iota=iota)
+        base = OS.topk_block_mask(sc, 0, sparse_ratio=0.75)
+        base[..., Kb - 1] = True
+        prot = np.zeros_like(base)
+        prot[..., Kb - 1] = True
+        assert float(store.pop("qk_pv_threshold")) == 1e10
+        _check_stats(store, OS.routing_stats(info, base.sum(-1), base, protected=prot), f"layer {layer}")
+
+
+@pytest.mark.parametrize("pool_mode", ["avg", "max"])
+def test_predict_attention_key_block_variance(pool_mode):
+    """The variance proxy of predict_attention (ATT:69-89) against the oracle
+    (pinned to the reference's own output by tests/test_golden.py)."""
+    from vasc_amd.attention import predict_attention
+    g = torch.Generator().manual_seed(5)
+    q = (torch.randn(1, 3, 1000, 64, generator=g) * 2).to(torch.bfloat16)
+    k = (torch.randn(1, 3, 1041, 64, generator=g) * 2).to(torch.bfloat16)
+    prob, var = predict_attention(q.cuda(), k.cuda(), pool_mode=pool_mode, return_key_block_variance=True)
+    assert torch.equal(prob, predict_attention(q.cuda(), k.cuda(), pool_mode=pool_mode))
+    ref = OP.key_block_variance(k.float().numpy())
+    assert var.shape == ref.shape == (1, 3, 17)
+    # the pooled bf16 means may differ by one bf16 ulp from a float64-summed mean
+    np.testing.assert_allclose(var.cpu().numpy(), ref, rtol=1e-2, atol=1e-3)

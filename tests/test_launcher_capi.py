@@ -114,6 +114,11 @@ def test_host_only_queries_and_argument_errors():
         + al(BH * P * 4)
     assert lib.vasc_select_workspace_size(1, BH, Q, K) == expect
     assert lib.vasc_select_workspace_size(0, 16, 259, 518) == 0
+    # result regions: row totals, row pair sums, capacities, then the admitted debt
+    offs = [lib.vasc_select_workspace_offset(1, BH, Q, K, r) for r in range(4)]
+    assert offs == [0, al(BH * Q * 4), 2 * al(BH * Q * 4), 3 * al(BH * Q * 4)]
+    assert lib.vasc_select_workspace_offset(1, BH, Q, K, 7) == -1
+    assert lib.vasc_select_workspace_offset(0, BH, Q, K, 0) == -1
     assert lib.vasc_packed_v_elems(1, 16, 33312, 64) == 16 * 521 * 64 * 64
     # validation happens before any HIP call: these return without a GPU
     rc = lib.vasc_pack_v(None, 0, 0, 8, 1, 1, 64, 64, None, None)

@@ -99,3 +99,22 @@ def test_pack_layer_order_of_operations():
     v_ref = x[:, :, 2].transpose(0, 2, 1, 3)
     assert np.array_equal(v, OL.reorder_to_patch_then_special(v_ref, N, P, S))
     assert k.shape == (1, H, N * P, D)
+
+
+@pytest.mark.parametrize("N,P,S", [(3, 11, 5), (2, 7, 0), (1, 6, 6)])
+def test_tokens_helpers_match_oracle(N, P, S):
+    """vasc_amd.tokens (the torch drop-in for the reference's
+    utils/tokens.py:2-126) against the oracle's index construction."""
+    import torch
+    from vasc_amd import tokens as T
+    x = np.random.default_rng(N * 10 + P).standard_normal((2, 3, N * P, 4)).astype(np.float32)
+    xt = torch.from_numpy(x)
+    assert np.array_equal(T.get_patch_tokens(xt, N, P, S).numpy(), OL.get_patch_tokens(x, N, P, S))
+    sp = T.get_special_tokens(xt, N, P, S)
+    ref_sp = OL.get_special_tokens(x, N, P, S)
+    assert (sp is None) == (ref_sp is None)
+    if sp is not None:
+        assert np.array_equal(sp.numpy(), ref_sp)
+    re = T.reorder_to_patch_then_special(xt, N, P, S)
+    assert np.array_equal(re.numpy(), OL.reorder_to_patch_then_special(x, N, P, S))
+    assert np.array_equal(T.restore_to_frame_major(re, N, P, S).numpy(), x)

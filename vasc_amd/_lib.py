@@ -16,6 +16,10 @@ LIB_PATH = Path(__file__).resolve().parent / "libvasc_hip.so"
 VASC_OK = 0
 MODE_TOPK = 0
 MODE_VASC = 1
+WS_ROW_TOTAL = 0
+WS_ROW_PAIR_SUM = 1
+WS_ROW_CAPACITY = 2
+WS_ADMITTED_DEBT = 3
 
 P = c_void_p
 I64 = c_int64
@@ -33,6 +37,7 @@ SIGNATURES: dict[str, tuple] = {
     "vasc_pooled_softmax_workspace_size": (I64, [I64, I64, I64, I64]),
     "vasc_pair_innovation": (c_int32, [P, I64, I64, I64, I64, P, P]),
     "vasc_select_workspace_size": (c_size_t, [I64, I64, I64, I64]),
+    "vasc_select_workspace_offset": (I64, [I64, I64, I64, I64, I32]),
     "vasc_select_blocks": (c_int32, [P, P, I64, I64, I64, I64, I32, I32, P, P, I32, I32, I32,
                                      P, P, P, P, P, P, P, P, P, P, I64, P, P, c_size_t, P]),
     "vasc_select_blocks_noalloc": (c_int32, [P, P, I64, I64, I64, I64, I32, I32, P, P, I32, I32, I32,

@@ -26,19 +26,32 @@ def predict_attention(query: torch.Tensor, key: torch.Tensor, ks_q: int = 128, k
 
     Pooled means are rounded to bf16 (block maxima are exact) and the logits
     follow the bf16 matmul of the reference's autocast run; the softmax is
-    fp32.
+    fp32. With ``return_key_block_variance`` also the per-key-block variance
+    proxy ``[B,H,Kb]`` (ATT:69-89): the block mean of the squared token norms
+    (squares rounded to the key dtype, float32 sums) minus the squared norm
+    of the bf16 block mean, clamped at 0.
     """
     assert pool_mode in ("max", "avg"), f"{pool_mode=}"
     assert query.ndim == 4 and key.ndim == 4
     if (ks_q, ks_k) != (ops.BLOCK_Q, ops.BLOCK_K):
         raise NotImplementedError("pooling is built for 128-token query and 64-token key blocks")
-    if return_key_block_variance:
-        raise NotImplementedError("key block variance feeds a research router that is not built")
     if pool_mode == "max":
         pq, pk = ops.pool_qk_max(query, key)
     else:
         pq, pk, _, _ = ops.pool_qkv(q=query, k=key, innovation=False)
-    return ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(query.shape[-1]))
+    prob = ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(query.shape[-1]))
+    if not return_key_block_variance:
+        return prob
+    mean = pk if pool_mode == "avg" else ops.pool_qkv(k=key, innovation=False)[1]
+    tok = (key * key).sum(dim=-1, dtype=torch.float32)  # squares in the key dtype, float32 sums: [B,H,Tk]
+    Tk = tok.shape[-1]
+    nb = mean.shape[-2]
+    padded = torch.nn.functional.pad(tok, (0, nb * ops.BLOCK_K - Tk))
+    count = torch.full((nb,), float(ops.BLOCK_K), device=tok.device)
+    count[-1] = Tk - (nb - 1) * ops.BLOCK_K
+    mean_sq = padded.view(*tok.shape[:-1], nb, ops.BLOCK_K).sum(-1) / count
+    var = (mean_sq - mean.float().square().sum(dim=-1)).clamp_min(0.0)
+    return prob, var
 
 
 _FRAME_GRID: contextvars.ContextVar = contextvars.ContextVar("vasc_frame_grid", default=None)

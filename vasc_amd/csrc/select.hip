@@ -1310,6 +1310,19 @@ extern "C" size_t vasc_select_workspace_size(int64_t B, int64_t H, int64_t q_blo
   return vasc::layout(B, H, q_blocks, k_blocks).bytes;
 }
 
+extern "C" int64_t vasc_select_workspace_offset(int64_t B, int64_t H, int64_t q_blocks, int64_t k_blocks,
+                                                int32_t region) {
+  if (B <= 0 || H <= 0 || q_blocks <= 0 || k_blocks <= 0) return -1;
+  const vasc::Workspace w = vasc::layout(B, H, q_blocks, k_blocks);
+  switch (region) {
+    case VASC_WS_ROW_TOTAL: return static_cast<int64_t>(w.total);
+    case VASC_WS_ROW_PAIR_SUM: return static_cast<int64_t>(w.rowpair);
+    case VASC_WS_ROW_CAPACITY: return static_cast<int64_t>(w.cap);
+    case VASC_WS_ADMITTED_DEBT: return static_cast<int64_t>(w.adm);
+    default: return -1;
+  }
+}
+
 namespace vasc {
 namespace {
 

@@ -117,6 +117,21 @@ def select_workspace(B: int, H: int, Q: int, K: int, device) -> torch.Tensor:
     return torch.empty(max(int(n), 256), device=device, dtype=torch.uint8)
 
 
+def select_workspace_region(workspace: torch.Tensor, B: int, H: int, Q: int, K: int, region: int) -> torch.Tensor:
+    """A result region of the VASC selection workspace after a VASC call
+    (``vasc_select_workspace_offset``): per-row totals, pair sums (float32
+    ``[B,H,Q]``), capacities (int32 ``[B,H,Q]``) or the admitted debt
+    (float32 ``[B,H,P]``)."""
+    off = int(_lib.fn("vasc_select_workspace_offset")(B, H, Q, K, int(region)))
+    if off < 0:
+        raise ValueError(f"unknown workspace region {region}")
+    P = (K + 1) // 2
+    n, dtype = {_lib.WS_ROW_TOTAL: (B * H * Q, torch.float32), _lib.WS_ROW_PAIR_SUM: (B * H * Q, torch.float32),
+                _lib.WS_ROW_CAPACITY: (B * H * Q, torch.int32), _lib.WS_ADMITTED_DEBT: (B * H * P, torch.float32)}[region]
+    shape = (B, H, P) if region == _lib.WS_ADMITTED_DEBT else (B, H, Q)
+    return workspace[off:off + 4 * n].view(dtype).view(shape)
+
+
 def select_blocks(score: torch.Tensor, *, mode: int, topk: int, innovation=None, row_cap=None,
                   protected_mask=None, force_last: bool = False, max_capacity: int = 0,
                   sink_blocks: int = 0, debt=None, pending_arrival=None, prev_service=None,
@@ -157,6 +172,7 @@ def select_blocks(score: torch.Tensor, *, mode: int, topk: int, innovation=None,
         out["gate"] = torch.empty(1, device=dev, dtype=torch.int32)
         if workspace is None:
             workspace = select_workspace(B, H, Q, K, dev)
+        out["workspace"] = workspace
     if want_priority:
         out["priority"] = torch.empty(B, H, Q, K, device=dev, dtype=torch.float32)
     if want_mask:

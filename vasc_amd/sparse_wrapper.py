@@ -245,15 +245,71 @@ def _pv_threshold(key: torch.Tensor, layer_idx: int) -> float | None:
     return thr
 
 
-def _stats(out: dict, cap: torch.Tensor | None) -> dict:
+def _counterfactual_stats() -> bool:
+    """SPARSE_VGGT_COSA_COUNTERFACTUAL_STATS (on unless set off, SW:3909-3912)."""
+    return os.environ.get("SPARSE_VGGT_COSA_COUNTERFACTUAL_STATS", "1").lower() in {"1", "true", "yes", "on"}
+
+
+def _routing_stats(score: torch.Tensor, out: dict, cap: torch.Tensor, base_mask: torch.Tensor, ledger_in: tuple,
+                   innovation: torch.Tensor, protected_mask: torch.Tensor | None, M: int) -> dict:
+    """The selector's routing statistics (SW:4032-4096) from the kernel's
+    outputs: ledger flow of the settlement (previous debt, settled arrival,
+    consumed service, reflection), the service gate, capacities, the QK
+    overlap with the base map and, with counterfactual statistics on (the
+    reference's default), the overlap of the current-only and debt
+    selections. The admitted debt is read back from the selection workspace.
+    Every value is a 0-d float32 tensor on the device."""
+    B, H, P = out["debt"].shape
+    Q, K = score.shape[-2:]
+    debt_in, pending, service = ledger_in
+    zeros = torch.zeros(B, H, P, device=score.device, dtype=torch.float32)
+    prev_before = zeros if debt_in is None else debt_in.float().reshape(B, H, P).clamp_min(0.0)
+    settled = zeros if pending is None else pending.float().reshape(B, H, P)
+    consumed = zeros if pending is None else service.float().reshape(B, H, P)
+    reflection = zeros if pending is None else (-((prev_before + settled) - consumed)).clamp_min(0.0)
+    previous = out["debt"]
+    useful = (consumed - reflection).clamp_min(0.0).sum()
+    wasted = reflection.sum()
+    consumed_total = consumed.sum()
+    utilization = torch.where(consumed_total > 0, useful / consumed_total.clamp_min(1e-8),
+                              torch.zeros_like(consumed_total))
+    admitted = ops.select_workspace_region(out["workspace"], B, H, Q, K, _lib.WS_ADMITTED_DEBT)
+    selected = out["mask"].bool()
+    denominator = cap.clamp_min(1).float()
+    overlap = (selected & base_mask).sum(dim=-1).float()
     stats = {
-        "cosa_pair_debt_enabled": torch.ones((), device=out["debt"].device),
+        "cosa_pair_debt_enabled": torch.ones((), device=score.device),
+        "cosa_pair_service_useful_repayment": useful,
+        "cosa_pair_service_wasted": wasted,
+        "cosa_pair_service_utilization": utilization,
         "cosa_pair_service_gate_debt": out["gate"].float().view(()),
-        "cosa_pair_arrival": out["arrival"].sum(-1).mean(),
-        "cosa_pair_backlog": out["debt"].sum(-1).mean(),
+        "cosa_pair_qk_capacity": cap.float().mean(),
+        "cosa_pair_arrival": out["arrival"].sum(dim=-1).mean(),
+        "cosa_pair_innovation": innovation.float().mean(),
+        "cosa_pair_debt_before_service": prev_before.mean(),
+        "cosa_pair_settled_arrival": settled.sum(dim=-1).mean(),
+        "cosa_pair_consumed_pv_service": consumed.sum(dim=-1).mean(),
+        "cosa_pair_admitted_debt": admitted.sum(dim=-1).mean(),
+        "cosa_pair_backlog": previous.sum(dim=-1).mean(),
+        "cosa_pair_qk_overlap": (overlap / denominator).mean(),
+        "cosa_pair_qk_swap_fraction": (1.0 - overlap / denominator).mean(),
+        "cosa_pair_budget_error": (selected.sum(dim=-1) - cap).abs().amax().float(),
+        "cosa_pair_conservation_error": (previous - prev_before - settled + consumed - reflection).abs().amax(),
     }
-    if cap is not None:
-        stats["cosa_pair_qk_capacity"] = cap.float().mean()
+    if _counterfactual_stats():
+        # current-only selection: the same arrival with no ledger (the gate
+        # stays closed, so the execution priority is the current priority)
+        cur = ops.select_blocks(score, mode=_lib.MODE_VASC, topk=0, innovation=innovation, row_cap=cap,
+                                protected_mask=protected_mask, max_capacity=M, want_mask=True, want_priority=True)
+        adm_k = admitted.repeat_interleave(2, dim=-1)[..., :K].unsqueeze(-2)
+        debt_priority = cur["priority"] + adm_k
+        if protected_mask is not None:
+            debt_priority = debt_priority.masked_fill(protected_mask.bool(), torch.finfo(torch.float32).max)
+        deb = ops.select_blocks(debt_priority, mode=_lib.MODE_TOPK, topk=0, row_cap=torch.clamp(cap, max=M),
+                                max_capacity=M, want_mask=True)
+        both = (cur["mask"].bool() & deb["mask"].bool()).sum(dim=-1).float()
+        stats["cosa_pair_current_debt_overlap"] = (both / denominator).mean()
+        stats["cosa_pair_history_swap_fraction"] = (1.0 - both / denominator).mean()
     return stats
 
 
@@ -316,7 +372,8 @@ def get_cosa_value_risk_pair_debt_mask(pooled_score: torch.Tensor, pooled_value:
                             prev_service=service, want_mask=True, want_priority=True)
     _ledger_outputs(routing_state, out, pooled_score, layer_idx, M, _service_domain())
     if stats_store is not None:
-        stats_store.update(_stats(out, cap))
+        stats_store.update(_routing_stats(pooled_score, out, cap, base_mask, (debt, pending, service), innovation,
+                                          protected_mask, M))
     return out["mask"].bool()
 
 
@@ -346,12 +403,15 @@ def finalize_cosa_value_risk_pair_debt(routing_state: dict | None, *, stats_stor
     terminal = ops.settle_terminal(prev, pending, service).view(pending.shape)
     routing_state[STATE_KEY] = terminal
     dev = terminal.device
+    previous = torch.zeros_like(pending) if prev is None else prev.float().clamp_min(0.0)
+    reflection = (-((previous + pending) - service)).clamp_min(0.0)
     stats = {
         "cosa_pair_terminal_settled": torch.tensor(1.0, device=dev),
         "cosa_pair_terminal_layer": torch.tensor(float(pending_layer), device=dev),
         "cosa_pair_terminal_arrival": pending.sum(dim=-1).mean(),
         "cosa_pair_terminal_service": service.sum(dim=-1).mean(),
         "cosa_pair_terminal_backlog": terminal.sum(dim=-1).mean(),
+        "cosa_pair_terminal_conservation_error": (terminal - previous - pending + service - reflection).abs().amax(),
     }
     if stats_store is not None:
         stats_store.update(stats)
@@ -410,19 +470,41 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
             if hint is None:
                 hint = max(t, 1) + int(force_last)
         debt, pending, service = _ledger_inputs(routing_state, B, H, P)
+        want_stats = routing_stats_store is not None
         sel = ops.select_blocks(pooled_score, mode=_lib.MODE_VASC, topk=t or 0, innovation=innovation,
                                 row_cap=base, force_last=force_last, max_capacity=hint, sink_blocks=sink, debt=debt,
                                 pending_arrival=pending, prev_service=service,
-                                want_priority=not cfg.skip_routing_stats)
-        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, min(hint, orig_kblk), cfg.service_domain)
-        if routing_stats_store is not None:
-            routing_stats_store.update(_stats(sel, None))
+                                want_priority=not cfg.skip_routing_stats, want_mask=want_stats)
+        M = min(hint, orig_kblk)
+        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, M, cfg.service_domain)
+        if want_stats:
+            # the base map the reference hands its selector: Top-K (or the
+            # cdf counts) plus the forced mixed tail (SW:7599-7662, 7750-7762)
+            if count is not None:
+                bm = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=0, row_cap=count,
+                                       force_last=force_last, want_mask=True)
+            else:
+                bm = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=t, force_last=force_last,
+                                       want_mask=True)
+            base_mask = bm["mask"].bool()
+            protected = None
+            if force_last:
+                protected = torch.zeros_like(base_mask)
+                protected[..., orig_kblk - 1] = True
+            routing_stats_store.update(_routing_stats(pooled_score, sel, base_mask.sum(-1, dtype=torch.int32),
+                                                      base_mask, (debt, pending, service), innovation, protected, M))
     elif count is not None:
         sel = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=0, row_cap=count, force_last=force_last,
                                 sink_blocks=sink)
     else:
         sel = ops.select_blocks(pooled_score, mode=_lib.MODE_TOPK, topk=t, force_last=force_last,
                                 sink_blocks=sink)
+    if routing_stats_store is not None:
+        # the layer's resolved PV threshold, 1e10 where it is inactive (SW:7012-7020, 7797-7800)
+        thr = resolve_pv_threshold(cfg.pv_threshold, Tk)
+        if not pv_threshold_active(cfg.pv_active_layers, layer_idx):
+            thr = 1e10
+        routing_stats_store["qk_pv_threshold"] = torch.tensor(thr, device=pooled_score.device)
     return sel, total_kblk
 
 
