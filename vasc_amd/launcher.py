@@ -1,7 +1,7 @@
 """Mode switch and structural layer-budget profile of the VASC launcher.
 
 Mirrors ``evaluate.py:12-80`` of the reference: the paper constants
-(``configs/paper.json``), ``layer_sparsity`` (favoured layers get ``s-delta``,
+(``vasc_amd/configs/paper.json``, the reference's ``configs/paper.json``), ``layer_sparsity`` (favoured layers get ``s-delta``,
 the others ``s + n_fav*delta/(L-n_fav)``, only above ``enable_above``),
 ``allocation_settings`` and ``method_environment`` (the ``SPARSE_VGGT_*``
 switches of the three release modes). ``routing_config`` resolves those
@@ -10,24 +10,17 @@ the reference's environment keep working.
 """
 from __future__ import annotations
 
+import json
 import math
 import os
 from dataclasses import dataclass
+from pathlib import Path
 
 MODES = ("dense", "topk", "vasc")
 
-CONFIG = {
-    "stride": 10,
-    "sparsities": [0.55, 0.65, 0.75, 0.85],
-    "pooling": {"query_tokens": 128, "key_tokens": 64, "children_per_pair": 2},
-    "structural": {
-        "enabled": True,
-        "enable_above": 0.70,
-        "delta": 0.05,
-        "vggt": {"layers": 24, "favored_layers_zero_based": [11, 12, 13, 14, 15, 16]},
-        "pi3": {"layers": 18, "favored_layers_zero_based": [12, 13, 14, 15, 16, 17]},
-    },
-}
+# The paper constants (the reference's configs/paper.json): evaluation stride,
+# the sparsity sweep and the structural layer-budget profile.
+CONFIG = json.loads((Path(__file__).resolve().parent / "configs" / "paper.json").read_text(encoding="utf-8"))
 
 
 def layer_sparsity_string(backbone: str, sparsity: float, allocation: str):
