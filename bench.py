@@ -425,6 +425,52 @@ def run_aggregator(dev, frames: int, ratios, steps: int, warmup: int, dense_reps
     return out
 
 
+def run_c1(dev, reps: int = 5) -> dict:
+    """Config 1 on the GPU: one global layer of 8 frames x 1041 tokens (H=16,
+    d=64; N(0,1) plus the per-frame rank-8 component) in vasc mode at
+    sparsity 0.75 with a fresh ledger (VGGT official mask), against dense
+    attention on the same layer: output differences and the median time of
+    ``reps`` calls of each (the vasc call includes pooling, selection with
+    the ledger, the V pack and the attention)."""
+    from vasc_amd import ops
+    from vasc_amd.attention import predict_attention
+    from vasc_amd.sparse_wrapper import block_sparse_attn_cuda
+    N, P, S, H, D = 8, 1041, 5, 16, 64
+    q, k, v = synthetic_layer(N, P, S, H, D, seed=0, device=dev)
+    n_patch = q.shape[2]
+
+    def vasc():
+        score = predict_attention(q, k[:, :, :n_patch])
+        return block_sparse_attn_cuda(q, k, v, score, sparse_ratio=0.75, return_sparsity=True, layer_idx=0,
+                                      routing_state={}, num_patch_tokens=n_patch)
+
+    def dense():
+        return ops.dense_attn(q, k, ops.pack_v(v))
+
+    times = {}
+    with _ModeEnv("vggt", "vasc"):
+        for name, fn in (("vasc", vasc), ("dense", dense)):
+            fn()
+            ms = []
+            for _ in range(reps):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                fn()
+                b.record()
+                torch.cuda.synchronize()
+                ms.append(a.elapsed_time(b))
+            times[name] = statistics.median(ms)
+        out, sparsity = vasc()
+    ref = dense().float()
+    diff = out.float() - ref
+    res = {"vasc_ms": times["vasc"], "dense_ms": times["dense"], "sparsity": float(sparsity),
+           "max_abs_vs_dense": float(diff.abs().max()), "mean_abs_vs_dense": float(diff.abs().mean()),
+           "rel_l2_vs_dense": float(diff.norm() / ref.norm())}
+    log(f"C1: vasc {res['vasc_ms']:.3f} ms, dense {res['dense_ms']:.3f} ms; vasc vs dense max-abs "
+        f"{res['max_abs_vs_dense']:.4f}, mean-abs {res['mean_abs_vs_dense']:.5f}, rel L2 {res['rel_l2_vs_dense']:.4f}")
+    return res
+
+
 def run_sparse_op(dev, N: int, ratios, steps: int, warmup: int, graph_mode: bool, dense: bool) -> dict:
     """The 24 global layers' sparse op alone (pool + pooled softmax, VASC
     selection with the chained ledger, V pack, block-sparse attention) on
@@ -787,6 +833,8 @@ def main() -> int:
     }
     if not args.no_sparse_op:
         result["sparse_op"] = run_sparse_op(dev, N, ratios, args.steps, args.warmup, args.graph, dense=True)
+    if args.workload == "c2":
+        result["c1"] = run_c1(dev)
     if not args.no_cpu_baseline and args.workload == "c2":
         result["cpu_baseline"] = cpu_baseline(N, ratios[0], L)
     print(json.dumps(result), flush=True)

@@ -163,8 +163,9 @@ int64_t vasc_select_workspace_offset(int64_t B, int64_t H, int64_t q_blocks,
  * gate_out    optional int32 scalar: 1 when the debt priority was used.
  * priority_out optional [B,H,Q,K] float32 execution priority.
  * mask_out    optional [B,H,Q,K] uint8 support of the patch blocks.
- * index_out   [B,H,Q,width] int32 ascending block indices (count entries
- *             valid, rest untouched); count_out [B,H,Q] int32.
+ * index_out   [B,H,Q,width] int32 ascending block indices: the kept patch
+ *             blocks, then the sink blocks (count entries in all), then -1
+ *             to the end of the row; count_out [B,H,Q] int32.
  * Built variant: K <= 8192.
  */
 int vasc_select_blocks(const float *score, const float *innovation,

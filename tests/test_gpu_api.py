@@ -140,20 +140,21 @@ def test_cosa_mask_api_chain_bit_exact(release_env):
 
 @pytest.mark.parametrize("model", ["vggt", "pi3"])
 def test_block_sparse_attn_c1_end_to_end(release_env, model):
-    """Config 1 (8 frames x 1041 tokens, H=16) through block_sparse_attn_cuda in
-    vasc mode, two chained layers; VGGT uses the official mask (no forced
-    tail), Pi3 protects the mixed tail block."""
+    """Config 1 (8 frames x 1041 tokens, H=16; N(0,1) plus the per-frame
+    rank-8 component of scale 0.5) through block_sparse_attn_cuda in vasc
+    mode, two chained layers; VGGT uses the official mask (no forced tail),
+    Pi3 protects the mixed tail block. The vasc-vs-dense difference of the
+    output is reported beside the parity check."""
+    import bench
+    from vasc_amd import ops
     from vasc_amd.attention import predict_attention
     from vasc_amd.sparse_wrapper import block_sparse_attn_cuda
     release_env(model, "vasc")
     N, P, S, H, D = 8, 1041, 5, 16, 64
     Np, Tk = N * (P - S), N * P
-    g = torch.Generator().manual_seed(4)
     st_gpu, st_ref = {}, {}
     for layer in range(2):
-        q = torch.randn(1, H, Np, D, generator=g).to(torch.bfloat16)
-        k = torch.randn(1, H, Tk, D, generator=g).to(torch.bfloat16)
-        v = torch.randn(1, H, Tk, D, generator=g).to(torch.bfloat16)
+        q, k, v = bench.synthetic_layer(N, P, S, H, D, seed=4 + layer, device="cpu")
         qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
         score = predict_attention(qc, kc[:, :, :Np])
         out, sparsity = block_sparse_attn_cuda(qc, kc, vc, score, sparse_ratio=0.75, return_sparsity=True,
@@ -168,8 +169,30 @@ def test_block_sparse_attn_c1_end_to_end(release_env, model):
         ref = OA.block_sparse_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), idx, cnt)
         err = np.abs(out.float().cpu().numpy() - ref)
         assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
+        dense = ops.dense_attn(qc, kc, ops.pack_v(vc)).float()
+        gap = (out.float() - dense).abs()
+        rel = float((out.float() - dense).norm() / dense.norm())
+        print(f"C1 {model} layer {layer}: vasc vs dense max-abs {float(gap.max()):.4f}, mean-abs "
+              f"{float(gap.mean()):.5f}, relative L2 {rel:.4f}, sparsity {float(sparsity):.4f}")
+        assert math.isfinite(rel)
         assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_debt"]),
                               np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
+        kb = -(-Np // 64)
+        _check_selected_indices(st_gpu, final, kb, int(kb * 0.25) + int(model == "pi3"))
+
+
+def _check_selected_indices(state, final, kb, M):
+    """routing_state's selected indices: width M (the capacity hint, as the
+    reference's ``max_patch_blocks``), each row's kept patch blocks ascending,
+    then the sink block ids kb.., then -1."""
+    got = state["cosa_value_risk_pair_selected_indices"].cpu().numpy()
+    assert state["cosa_value_risk_pair_max_patch_blocks"] == M and got.shape == final.shape[:-1] + (M,)
+    sink = final.shape[-1] - kb
+    rows_final = final.reshape(-1, final.shape[-1])
+    for r, row in enumerate(got.reshape(-1, M)):
+        kept = np.flatnonzero(rows_final[r, :kb])
+        expect = np.concatenate([kept, kb + np.arange(sink), np.full(M, -1)])[:M]
+        assert np.array_equal(row, expect), r
 
 
 @pytest.mark.parametrize("model,mode", [("pi3", "topk"), ("pi3", "vasc"), ("vggt", "vasc")])

@@ -1148,6 +1148,7 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
       compact_row<kVasc, true, EPT>(key, lane, T, need, split, none, tsel, nullptr, 0, nullptr,
                                     p.mask_out + row * p.K);
     for (int i = lane; i < p.sink && run_sel + i < p.width; i += 64) irow[run_sel + i] = static_cast<int32_t>(p.K + i);
+    for (int64_t e = run_sel + p.sink + lane; e < p.width; e += 64) irow[e] = -1;  // the rest of the row defined
     if (lane == 0) p.count_out[row] = run_sel + p.sink;
   }
   if (kVasc) {

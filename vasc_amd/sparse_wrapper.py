@@ -16,8 +16,14 @@ Mirrors the operator surface of the reference's
 Every function runs the HIP kernels of ``libvasc_hip.so``; CPU tensors are
 rejected. Documented differences from the reference: attention computes in
 bf16 with fp32 accumulation (the reference quantises Q/K to int8 and P to
-fp16); ``routing_state["cosa_value_risk_pair_selected_indices"]`` holds the
-ascending index lists (the reference stores them in priority order); ties in
+fp16); ``routing_state["cosa_value_risk_pair_selected_indices"]`` ([B,H,Q,M]
+int32) holds each row's kept patch blocks in ascending order, then the sink
+block ids K.. and -1 to width M (the reference stores ``priority.topk(M)``
+indices in descending priority, SW:3890-3894); M
+(``cosa_value_risk_pair_max_patch_blocks``) is the capacity hint with a
+ratio, as in the reference, and ``max(topk, 1) + force_last`` with an
+explicit ``topk`` where the reference reads the largest row capacity back to
+the host (equal unless every row already keeps the mixed-tail block); ties in
 the selection go to the lower block index (``torch.topk`` leaves them
 unspecified).
 """
