@@ -811,15 +811,11 @@ __device__ __forceinline__ int sample_margin(int S, int c, int K) {
 // step follows every element of lower lanes and its own j' < j; ties at T
 // are kept in index order up to need when split. The kept indices go to
 // stage[0 ..) in LDS (other lanes write their trash slot stage[64 EPT +
-// lane]) and, for VASC, into the pair counts: two 16-bit counts per word
-// (pair p in half p % 2 of word p / 2; a workgroup's rows give each pair at
-// most 2 * rows_per_workgroup), trash counters in the 64 words after them.
-// kMask: writes the 0/1 mask (every element of the row) instead.
+// lane]). kMask: writes the 0/1 mask (every element of the row) instead.
 // Returns the number kept.
-template <bool kVasc, bool kMask, int EPT>
+template <bool kMask, int EPT>
 __device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane, uint32_t T, int need, bool split,
-                                           bool none, uint32_t tsel, uint32_t *stage, int P, uint32_t *pair_cnt,
-                                           uint8_t *mrow) {
+                                           bool none, uint32_t tsel, uint32_t *stage, uint8_t *mrow) {
   int run_sel = 0, run_eq = 0;
 #pragma unroll
   for (int i = 0; i < EPT / 4; ++i) {
@@ -862,15 +858,22 @@ __device__ __forceinline__ int compact_row(const uint32_t (&key)[EPT], int lane,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         stage[sel[j] ? pos : 64 * EPT + lane] = static_cast<uint32_t>(kk + j);
-        // pair p counts in half p % 2 of word p / 2; the trash words follow
-        if (kVasc) atomicAdd(&pair_cnt[sel[j] ? (kk + j) >> 2 : ((P + 1) >> 1) + lane],
-                             sel[j] ? 1u << (((kk + j) & 2) << 3) : 1u);
         pos += sel[j] ? 1 : 0;
         run_sel += __popcll(bsel[j]);
       }
     }
   }
   return run_sel;
+}
+
+// 256-element steps that are whole in every row an instance is launched for:
+// launch_select_mode picks the instance for K in (64 * E', 64 * EPT], E'
+// the next smaller instance, so the first E' / 4 steps never reach the row
+// end and need no per-step branch.
+template <int EPT>
+constexpr int full_steps() {
+  return EPT == 8 ? 1 : EPT == 12 ? 2 : EPT == 16 ? 3 : EPT == 24 ? 4 : EPT == 32 ? 6 : EPT == 36 ? 8
+       : EPT == 48 ? 9 : EPT == 64 ? 12 : EPT == 96 ? 16 : EPT == 128 ? 24 : 0;
 }
 
 // per wave: histogram (256 bins + 64 per-lane trash bins), small-bin keys
@@ -898,7 +901,7 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
   const int K = static_cast<int>(p.K);
   int gate = 0;
   if (kVasc) {
-    for (int64_t i = tid; i < (p.P + 1) / 2 + 64; i += 256) pair_cnt[i] = 0;  // packed pairs + 64 trash counters
+    for (int64_t i = tid; i < (p.P + 1) / 2; i += 256) pair_cnt[i] = 0;  // packed pair counts
     __syncthreads();
     gate = service_gate(p);
   }
@@ -927,7 +930,7 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
 #pragma unroll
     for (int i = 0; i < EPT / 4; ++i) {
       const int kk = 256 * i + 4 * lane;
-      if (256 * (i + 1) <= K) {
+      if (i < full_steps<EPT>() || 256 * (i + 1) <= K) {
         const u32x4u x = *reinterpret_cast<const u32x4u *>(srow + kk);
 #pragma unroll
         for (int j = 0; j < 4; ++j) key[4 * i + j] = x[j];
@@ -1019,7 +1022,7 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
     };
 #pragma unroll
     for (int i = 0; i < EPT / 4; ++i) {
-      if (256 * (i + 1) < K)
+      if (i < full_steps<EPT>() || 256 * (i + 1) < K)
         transform(i, std::false_type{});
       else if (256 * i < K)
         transform(i, std::true_type{});
@@ -1136,17 +1139,20 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
     // mask and priority outputs in passes of their own
     int32_t *irow = p.index_out + row * p.width;
     asm volatile("" : "+v"(lane));  // element indices recomputed here, not kept from the loads
-    const int run_sel = compact_row<kVasc, false, EPT>(key, lane, T, need, split, none, tsel, cand,
-                                                      static_cast<int>(p.P), pair_cnt, nullptr);
+    const int run_sel = compact_row<false, EPT>(key, lane, T, need, split, none, tsel, cand, nullptr);
     wave_sync();
-    {
-      const int wn = run_sel < p.width ? run_sel : static_cast<int>(p.width);
-      for (int e = lane; e < wn; e += 64) irow[e] = static_cast<int32_t>(cand[e]);  // coalesced
+    // the staged list to the index row (coalesced) and, for VASC, into the
+    // workgroup's pair counts: two 16-bit counts per word (pair p in half
+    // p % 2 of word p / 2; a workgroup's rows give each pair at most
+    // 2 * rows_per_workgroup)
+    for (int e = lane; e < run_sel; e += 64) {
+      const uint32_t kb = cand[e];
+      if (e < p.width) irow[e] = static_cast<int32_t>(kb);
+      if (kVasc) atomicAdd(&pair_cnt[kb >> 2], 1u << ((kb & 2u) << 3));
     }
     wave_sync();  // the staged list is read before the next row reuses it
     if (p.mask_out)
-      compact_row<kVasc, true, EPT>(key, lane, T, need, split, none, tsel, nullptr, 0, nullptr,
-                                    p.mask_out + row * p.K);
+      compact_row<true, EPT>(key, lane, T, need, split, none, tsel, nullptr, p.mask_out + row * p.K);
     for (int i = lane; i < p.sink && run_sel + i < p.width; i += 64) irow[run_sel + i] = static_cast<int32_t>(p.K + i);
     for (int64_t e = run_sel + p.sink + lane; e < p.width; e += 64) irow[e] = -1;  // the rest of the row defined
     if (lane == 0) p.count_out[row] = run_sel + p.sink;
@@ -1217,7 +1223,7 @@ int launch_select_cfg(const SelectParams &p, hipStream_t s) {
   const int64_t rows = p.BH * p.Q;
   const int rpw = static_cast<int>(rows >= 4 * 8192 ? 4 : (rows >= 2 * 8192 ? 2 : 1));
   const size_t lds_bytes =
-      (static_cast<size_t>(kWaves) * wave_lds_words<EPT>() + (kVasc ? static_cast<size_t>(p.P + 1) / 2 + 64 : 0)) * 4;
+      (static_cast<size_t>(kWaves) * wave_lds_words<EPT>() + (kVasc ? static_cast<size_t>(p.P + 1) / 2 : 0)) * 4;
   const void *kern = reinterpret_cast<const void *>(select_kernel<kVasc, EPT>);
   int rc;
   if ((rc = reserve_lds(kern, lds_bytes))) return rc;
