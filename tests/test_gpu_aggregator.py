@@ -199,14 +199,17 @@ class _Env:
         os.environ.update(self.saved)
 
 
-def test_dense_aggregator_matches_torch_float32():
-    agg = _model(Aggregator, dim=128, depth=2, num_heads=2, mlp_ratio=2.0, intermediate_layer_idx=(1,))
+@pytest.mark.parametrize("dim", [128, 512])
+def test_dense_aggregator_matches_torch_float32(dim):
+    """dim 512 runs the fused residual + LayerNorm passes (vasc_residual_norm)
+    between the sub-layers; dim 128 the separate torch ops."""
+    agg = _model(Aggregator, dim=dim, depth=2, num_heads=dim // 64, mlp_ratio=2.0, intermediate_layer_idx=(1,))
     images = _images()
     with torch.no_grad():
         ref = _ref_aggregator(agg, images)
         outs, start = agg.to(torch.bfloat16)(images)
     assert start == 5 and outs[0] is None and outs[1] is not None
-    _close(outs[-1][..., 128:], ref)
+    _close(outs[-1][..., dim:], ref)
 
 
 def test_sparse_install_at_zero_sparsity_is_dense():
@@ -249,11 +252,12 @@ def test_pi3_decoder_topk_runs_and_zero_sparsity_is_dense():
     _close(sparse, dense.float())
 
 
-def test_vasc_aggregator_matches_torch_float32_on_its_lists(monkeypatch):
+@pytest.mark.parametrize("dim", [128, 512])
+def test_vasc_aggregator_matches_torch_float32_on_its_lists(dim, monkeypatch):
     """VGGT-shaped aggregator in vasc mode with the structural-style per-layer
     ratios: output vs the float32 restatement over the recorded lists, and the
     lists vs the oracle's VASC chain (official mask: no forced tail)."""
-    agg = _model(Aggregator, dim=128, depth=3, num_heads=2, mlp_ratio=2.0, intermediate_layer_idx=(2,))
+    agg = _model(Aggregator, dim=dim, depth=3, num_heads=dim // 64, mlp_ratio=2.0, intermediate_layer_idx=(2,))
     images = _images(N=6, H=112, W=126)
     ratios = [0.75, 0.6, 0.8]
     rec = _Recorder(monkeypatch)
@@ -268,15 +272,15 @@ def test_vasc_aggregator_matches_torch_float32_on_its_lists(monkeypatch):
         for r in rec.layers:  # the lists are sparse: some blocks left out in every layer
             assert int(r["count"].sum()) < r["count"].numel() * (-(-6 * P // 64))
         ref = _ref_aggregator(agg, images, rec.layers)
-    _close(outs[-1][..., 128:], ref)
+    _close(outs[-1][..., dim:], ref)
 
 
-@pytest.mark.parametrize("mode", ["vasc", "topk"])
-def test_pi3_decoder_sparse_matches_torch_float32_on_its_lists(mode, monkeypatch):
+@pytest.mark.parametrize("mode,dim", [("vasc", 128), ("topk", 128), ("vasc", 512)])
+def test_pi3_decoder_sparse_matches_torch_float32_on_its_lists(mode, dim, monkeypatch):
     """Pi3-shaped decoder (6 blocks, odd ones global, 5 register tokens, the
     mixed tail protected): output vs the float32 restatement over the recorded
     lists, lists vs the oracle chain; dense vs the restatement without lists."""
-    model = _model(Pi3Decoder, dim=128, depth=6, num_heads=2, mlp_ratio=2.0).to(torch.bfloat16)
+    model = _model(Pi3Decoder, dim=dim, depth=6, num_heads=dim // 64, mlp_ratio=2.0).to(torch.bfloat16)
     images = _images(N=5, H=98, W=126, seed=3)
     P = 5 + 7 * 9
     rec = _Recorder(monkeypatch)

@@ -87,7 +87,7 @@ def test_allocation_settings():
 
 # ------------------------------------------------------------------ C-ABI
 def _header_functions():
-    text = (ROOT / "include" / "vasc_hip.h").read_text()
+    text = "".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
     return set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(vasc_\w+)\s*\(", text, flags=re.M))
 
 
@@ -97,7 +97,7 @@ def test_library_exports_every_declared_symbol():
     assert len(names) >= 12
     for name in names:
         assert hasattr(lib, name), name
-    assert names == set(_lib.SIGNATURES), "ctypes table out of sync with include/vasc_hip.h"
+    assert names == set(_lib.SIGNATURES), "ctypes table out of sync with include/*.h"
     assert lib.vasc_abi_version() == 5
 
 
@@ -158,6 +158,15 @@ def test_host_only_queries_and_argument_errors():
     rc = lib.vasc_block_sparse_attn_pv_fwd(None, 0, 0, 8, None, 0, 0, 8, None, None, 0, 0, 8, 1, 1, 128, 64, 64,
                                            None, 1, None, 0, ctypes.c_float(0.125), None, None, None)
     assert rc == 1 and b"pv_threshold" in lib.vasc_last_error()
+    # runner op: built widths, required rows, outputs and alignment
+    rc = lib.vasc_residual_norm(fake, 1000, fake, 1000, None, None, None, f(1e-6), fake, 1000, None, 0, 4, 1000, None)
+    assert rc == 2 and b"not built" in lib.vasc_last_error()
+    rc = lib.vasc_residual_norm(fake, 1024, None, 1024, None, None, None, f(1e-6), fake, 1024, None, 0, 4, 1024, None)
+    assert rc == 1 and b"y is NULL" in lib.vasc_last_error()
+    rc = lib.vasc_residual_norm(fake, 1024, fake, 1024, None, None, None, f(1e-6), None, 0, None, 0, 4, 1024, None)
+    assert rc == 1 and b"both NULL" in lib.vasc_last_error()
+    rc = lib.vasc_residual_norm(fake, 1000, fake, 1024, None, None, None, f(1e-6), fake, 1024, None, 0, 4, 1024, None)
+    assert rc == 1 and b"row stride" in lib.vasc_last_error()
 
 
 def test_select_rejects_ledger_aliasing():

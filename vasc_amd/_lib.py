@@ -25,7 +25,7 @@ P = c_void_p
 I64 = c_int64
 I32 = c_int32
 
-# name -> (restype, argtypes); mirrors include/vasc_hip.h.
+# name -> (restype, argtypes); mirrors include/vasc_hip.h and include/vasc_runner.h.
 SIGNATURES: dict[str, tuple] = {
     "vasc_last_error": (ctypes.c_char_p, []),
     "vasc_abi_version": (c_int32, []),
@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple] = {
                                 P, I64, I64, P, P, I64, P, P, P, P, P]),
     "vasc_restore_tokens": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64, I64, I64,
                                       P, P]),
+    # include/vasc_runner.h
+    "vasc_residual_norm": (c_int32, [P, I64, P, I64, P, P, P, c_float, P, I64, P, I64, I64, I64, P]),
 }
 
 _lock = threading.Lock()

@@ -167,9 +167,31 @@ class Block(nn.Module):
         self.mlp = Mlp(dim, int(dim * mlp_ratio))
         self.ls2 = LayerScale(dim, init_values)
 
-    def forward(self, x: torch.Tensor, pos: torch.Tensor | None = None) -> torch.Tensor:
-        x = x + self.ls1(self.attn(self.norm1(x), pos=pos))
-        return x + self.ls2(self.mlp(self.norm2(x)))
+    def forward(self, x: torch.Tensor, pos: torch.Tensor | None = None, *, normed: torch.Tensor | None = None,
+                next_norm: nn.LayerNorm | None = None):
+        """``normed``: ``norm1(x)`` when the caller already has it; with
+        ``next_norm`` also returns ``next_norm`` of the output (the next
+        block's first norm), as ``(out, normed_out)``. On the GPU in bf16
+        each residual update runs with the norm after it as one
+        ``vasc_residual_norm`` pass, rounded as the separate torch ops."""
+        h = self.norm1(x) if normed is None else normed
+        a = self.attn(h, pos=pos)
+        if not _fused_residual(x, a):
+            x = x + self.ls1(a)
+            x = x + self.ls2(self.mlp(self.norm2(x)))
+            return x if next_norm is None else (x, next_norm(x))
+        x, h2 = ops.residual_norm(x, a, self.ls1.gamma, _ln(self.norm2))
+        x, nxt = ops.residual_norm(x, self.mlp(h2), self.ls2.gamma, _ln(next_norm) if next_norm is not None else None)
+        return x if next_norm is None else (x, nxt)
+
+
+def _fused_residual(x: torch.Tensor, y: torch.Tensor) -> bool:
+    return (x.is_cuda and x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16 and x.shape == y.shape
+            and x.shape[-1] in (512, 1024, 1536, 2048))
+
+
+def _ln(norm: nn.LayerNorm):
+    return (norm.weight, norm.bias, norm.eps)
 
 
 def grid_positions(frames: int, h: int, w: int, special: int, device) -> torch.Tensor:
@@ -228,13 +250,21 @@ class Aggregator(nn.Module):
         tokens = torch.cat([*(s.to(tokens.dtype) for s in special), tokens], dim=1)
         h, w = Hi // self.patch_size, Wi // self.patch_size
         P, C = tokens.shape[1], tokens.shape[2]
-        pos = grid_positions(B * N, h, w, self.patch_start_idx, images.device)
+        # int32 positions made once: the layers' layout kernel reads them as they are
+        pos = grid_positions(B * N, h, w, self.patch_start_idx, images.device).to(torch.int32).contiguous()
+        pos_global = pos.view(B, N * P, 2)
         outputs = []
+        normed = None  # the next block's norm1 of the tokens, from the previous block's last pass
         with frame_grid(h, w):
             for i in range(self.aa_block_num):
-                tokens = self.frame_blocks[i](tokens.view(B * N, P, C), pos=pos)
+                fb, gb = self.frame_blocks[i], self.global_blocks[i]
+                tokens, normed = fb(tokens.view(B * N, P, C), pos=pos, normed=normed, next_norm=gb.norm1)
                 frame_out = tokens.view(B, N, P, C)
-                tokens = self.global_blocks[i](tokens.view(B, N * P, C), pos=pos.reshape(B, N * P, 2))
+                nxt = self.frame_blocks[i + 1].norm1 if i + 1 < self.aa_block_num else None
+                out = gb(tokens.view(B, N * P, C), pos=pos_global, normed=normed.view(B, N * P, C), next_norm=nxt)
+                tokens, normed = out if nxt is not None else (out, None)
+                if normed is not None:
+                    normed = normed.view(B * N, P, C)
                 if i in self.intermediate_layer_idx:
                     outputs.append(torch.cat([frame_out, tokens.view(B, N, P, C)], dim=-1))
                 else:
@@ -274,15 +304,19 @@ class Pi3Decoder(nn.Module):
         hidden = torch.cat([reg.to(hidden.dtype), hidden], dim=1)
         hw = hidden.shape[1]
         h, w = H // self.patch_size, W // self.patch_size
-        pos = grid_positions(B * N, h, w, self.patch_start_idx, hidden.device)
+        pos = grid_positions(B * N, h, w, self.patch_start_idx, hidden.device).to(torch.int32).contiguous()
+        pos_frame, pos_global = pos.view(B * N, hw, 2), pos.view(B, N * hw, 2)
         final = []
+        normed = None  # the next block's norm1, from the previous block's last pass
+        depth = len(self.decoder)
         with frame_grid(h, w):
             for i, blk in enumerate(self.decoder):
-                if i % 2 == 0:
-                    hidden = blk(hidden.reshape(B * N, hw, C), pos=pos.reshape(B * N, hw, 2))
-                else:
-                    hidden = blk(hidden.reshape(B, N * hw, C), pos=pos.reshape(B, N * hw, 2))
-                if i + 1 in (len(self.decoder) - 1, len(self.decoder)):
+                shape = (B * N, hw, C) if i % 2 == 0 else (B, N * hw, C)
+                nxt = self.decoder[i + 1].norm1 if i + 1 < depth else None
+                out = blk(hidden.reshape(shape), pos=pos_frame if i % 2 == 0 else pos_global,
+                          normed=normed.view(shape) if normed is not None else None, next_norm=nxt)
+                hidden, normed = out if nxt is not None else (out, None)
+                if i + 1 in (depth - 1, depth):
                     final.append(hidden.reshape(B * N, hw, C))
         _finalize(self)
         return torch.cat(final, dim=-1), pos

@@ -356,6 +356,69 @@ def _btht(t: torch.Tensor, name: str) -> tuple:
     return t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)
 
 
+_PARAM_CACHE: dict = {}
+
+
+def _param_as(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """A small parameter as a contiguous ``dtype`` tensor on its device,
+    converted once per (storage, version): repeated layer calls then launch
+    no conversion kernels. The entry keeps the source alive, so its address
+    cannot be reused while cached; an in-place update bumps the version."""
+    t = t.detach()
+    if t.dtype == dtype and t.is_contiguous():
+        return t
+    key = (t.data_ptr(), t._version, t.dtype, dtype, tuple(t.shape), tuple(t.stride()))
+    hit = _PARAM_CACHE.get(key)
+    if hit is not None:
+        return hit[1]
+    if len(_PARAM_CACHE) > 4096:
+        _PARAM_CACHE.clear()
+    conv = t.to(dtype).contiguous()
+    _PARAM_CACHE[key] = (t, conv)
+    return conv
+
+
+def residual_norm(x: torch.Tensor, y: torch.Tensor, gamma: torch.Tensor | None = None, norm=None):
+    """Residual update of a pre-norm block and the next LayerNorm in one pass:
+    ``x_new = bf16(x + bf16(y * gamma))`` (torch's bf16 LayerScale multiply and
+    add) and, with ``norm = (weight or None, bias or None, eps)``, its
+    LayerNorm over the last dimension (fp32 statistics, bf16 output).
+    x, y: ``[..., dim]`` bf16 of one shape; gamma, weight, bias: ``[dim]``.
+    Returns ``(x_new, normed or None)``; x is not modified."""
+    _dev(x, "x")
+    _dev(y, "y")
+    if x.shape != y.shape:
+        raise ValueError(f"x {tuple(x.shape)} and y {tuple(y.shape)} differ")
+    if x.dtype != torch.bfloat16 or y.dtype != torch.bfloat16:
+        raise ValueError("residual_norm computes on bf16 rows")
+    dim = x.shape[-1]
+    xr, yr = x.reshape(-1, dim), y.reshape(-1, dim)
+    if xr.stride(-1) != 1:
+        xr = xr.contiguous()
+    if yr.stride(-1) != 1:
+        yr = yr.contiguous()
+    rows = xr.shape[0]
+    keep = []
+
+    def param(t, name):
+        if t is None:
+            return None
+        if t.numel() != dim:
+            raise ValueError(f"{name} must hold {dim} values")
+        t = _param_as(t, torch.bfloat16)
+        _dev(t, name)
+        keep.append(t)
+        return t.data_ptr()
+
+    xo = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+    no = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16) if norm is not None else None
+    w, b, eps = norm if norm is not None else (None, None, 0.0)
+    _lib.call("vasc_residual_norm", xr.data_ptr(), xr.stride(0), yr.data_ptr(), yr.stride(0), param(gamma, "gamma"),
+              param(w, "norm weight"), param(b, "norm bias"), float(eps), xo.data_ptr(), dim,
+              no.data_ptr() if no is not None else None, dim, rows, dim, _stream())
+    return xo, no
+
+
 def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, frames: int, tokens_per_frame: int,
              special: int, *, q_norm=None, k_norm=None, pos: torch.Tensor | None = None,
              rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None):
@@ -386,9 +449,9 @@ def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, frames: int, tok
             if t is None:
                 out.append(None)
             else:
-                t = t.detach().float().contiguous()
                 if t.numel() != D:
                     raise ValueError(f"{name} parameters must hold {D} values")
+                t = _param_as(t, torch.float32)
                 _dev(t, name)
                 keep.append(t)
                 out.append(t.data_ptr())
