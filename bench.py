@@ -341,7 +341,23 @@ class _ModeEnv:
         os.environ.update(self.saved)
 
 
-def run_aggregator(dev, frames: int, ratios, steps: int, warmup: int, dense_reps: int = 3) -> dict:
+def tune_gemms(enable: bool) -> None:
+    """torch's TunableOp for the runners' hipBLASLt GEMMs: each GEMM shape is
+    tuned (at most 30 trials or 200 ms) the first time it runs, in the dense
+    warm-up forward, and the choice is reused by every later call. The
+    results file goes to the temporary directory."""
+    import tempfile
+    import torch.cuda.tunable as tunable
+    tunable.enable(enable)
+    tunable.tuning_enable(enable)
+    if enable:
+        tunable.set_max_tuning_duration(200)
+        tunable.set_max_tuning_iterations(30)
+        tunable.set_filename(os.path.join(tempfile.gettempdir(), f"vasc_tunableop_{os.getpid()}.csv"))
+
+
+def run_aggregator(dev, frames: int, ratios, steps: int, warmup: int, dense_reps: int = 3,
+                   tune: bool = True) -> dict:
     """The VGGT-shaped aggregator (24 frame + 24 global blocks, dim 1024, 16
     heads, MLP 4096, random init bf16) on seeded uniform-noise images
     ``[1, frames, 3, 392, 518]``.
@@ -354,6 +370,10 @@ def run_aggregator(dev, frames: int, ratios, steps: int, warmup: int, dense_reps
       CudaAttentionTimer scope, eval_7scenes_sparse_vggt.py:1533-1574: qkv,
       layout, sparse op, restore, proj) and around every attention launch
       (the roofline's kernel).
+
+    The block GEMMs (qkv, proj, fc1, fc2) run on hipBLASLt through torch;
+    with ``tune`` torch's TunableOp picks their algorithms in the first
+    (untimed) dense forward.
     """
     from vasc_amd import install
     agg = build_aggregator(dev)
@@ -392,7 +412,12 @@ def run_aggregator(dev, frames: int, ratios, steps: int, warmup: int, dense_reps
         return a.elapsed_time(b), per_fwd
 
     out = {}
-    forwards(1, False)
+    tune_gemms(tune)
+    forwards(1, False)  # the warm-up forward tunes the GEMM shapes
+    if tune:
+        import torch.cuda.tunable as tunable
+        tunable.tuning_enable(False)
+        out["gemm_tuning"] = {"TunableOp": True, "tuned": len(tunable.get_results())}
     total, glob = forwards(dense_reps, True)
     out["dense"] = {"forward_ms": total / dense_reps, "frames_per_s": frames / (total / dense_reps * 1e-3),
                     "global_attn_ms_per_forward": statistics.median(glob),
@@ -591,7 +616,7 @@ def smooth_images(frames: int, seed: int, dev) -> torch.Tensor:
     return torch.nn.functional.interpolate(low, size=(392, 518), mode="bilinear", align_corners=False).unsqueeze(0)
 
 
-def run_c4(dev, steps: int, warmup: int) -> dict:
+def run_c4(dev, steps: int, warmup: int, tune: bool = True) -> dict:
     """C4: the Pi3-shaped decoder (36 blocks, odd ones global, dim 1024, 16
     heads, 5 register tokens, no camera token, random init bf16) on 64
     frames of seeded smooth noise: dense, then vasc and topk at sparsity 0.75
@@ -619,8 +644,13 @@ def run_c4(dev, steps: int, warmup: int) -> dict:
         return y, a.elapsed_time(b) / n
 
     res = {}
+    tune_gemms(tune)
     with torch.no_grad():
-        forwards(1)
+        forwards(1)  # the warm-up forward tunes the GEMM shapes
+    if tune:
+        import torch.cuda.tunable as tunable
+        tunable.tuning_enable(False)
+    with torch.no_grad():
         dense_out, dense_ms = forwards(max(1, steps // 2))
     res["dense"] = {"forward_ms": dense_ms, "frames_per_s": frames / (dense_ms * 1e-3)}
     log(f"C4 dense: forward {dense_ms:.2f} ms")
@@ -726,6 +756,8 @@ def main() -> int:
                          "decoder at 64 frames; c5: per-kernel microbenchmarks at T = 16k/64k/256k")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sparse-op", action="store_true", help="skip the 24-layer sparse-op step (extras)")
+    ap.add_argument("--no-gemm-tuning", dest="tune", action="store_false", default=True,
+                    help="keep torch's default hipBLASLt GEMM choice (no TunableOp pass in the warm-up)")
     ap.add_argument("--no-graph", dest="graph", action="store_false", default=True,
                     help="time the sparse-op step eagerly only (no HIP graph replay)")
     ap.add_argument("--probe", choices=("attention", "aggregator", "traffic"),
@@ -773,7 +805,7 @@ def main() -> int:
         return 0
 
     if args.workload == "c4":
-        c4 = run_c4(dev, args.steps, args.warmup)
+        c4 = run_c4(dev, args.steps, args.warmup, tune=args.tune)
         v = c4["vasc"]
         result = {
             "metric": "Pi3-shaped decoder forward, vasc @75% sparsity, 64 frames; frames/s",
@@ -783,14 +815,16 @@ def main() -> int:
             "data": "synthetic: seeded smooth noise (28x37 uniform noise bilinearly upsampled to 392x518)",
             "config": {"workload": "C4 Pi3-shaped decoder forward (36 blocks, 18 global), vasc and topk vs dense",
                        "frames": frames, "tokens": frames * 1041, "heads": 16, "head_dim": 64, "dim": 1024,
-                       "sparsity": sparsity, "structural_allocation": True},
+                       "sparsity": sparsity, "structural_allocation": True,
+                       "block_gemms": "hipBLASLt via torch" + (", TunableOp-tuned in the warm-up" if args.tune else "")},
             "c4": c4,
         }
         print(json.dumps(result), flush=True)
         return 0
 
     N, P, S, H, D, L = frames, 1041, 5, 16, 64, 24
-    agg = run_aggregator(dev, N, ratios, args.steps, args.warmup, dense_reps=3 if args.workload == "c2" else 1)
+    agg = run_aggregator(dev, N, ratios, args.steps, args.warmup, dense_reps=3 if args.workload == "c2" else 1,
+                         tune=args.tune)
     v = agg["vasc"]
     achieved = agg["attn_flops_per_launch"] / (agg["attn_ms_per_launch"] * 1e-3) / 1e12
     result = {
@@ -812,6 +846,7 @@ def main() -> int:
                         f"dim 1024, 16 heads, MLP 4096) with the vasc sparse global attention",
             "frames": N, "tokens": N * P, "patch_tokens": N * (P - S), "heads": H, "head_dim": D,
             "global_layers": L, "mode": "vasc", "sparsity": sparsity, "structural_allocation": True,
+            "block_gemms": "hipBLASLt via torch" + (", TunableOp-tuned in the warm-up" if args.tune else ""),
         },
         "global_layer_ms": v["global_layer_ms"],
         "frames_per_s_global_layers": v["frames_per_s_global_layers"],

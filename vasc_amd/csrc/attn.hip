@@ -252,21 +252,26 @@ void bsattn_fwd_kernel(const AttnParams p) {
     }
     return bs0 + bs1;
   };
-  // Slow path for the current block: mask keys that do not exist, move m to
+  // Scores of keys at or past lim (of the block's 64) to -inf. An opaque
+  // copy of the lane's key offset keeps the 32 per-element key indices from
+  // being hoisted out of the loop.
+  auto mask_keys = [&](floatx16 (&S)[2], int lim) {
+    int h4 = 4 * hf;
+    asm volatile("" : "+v"(h4));
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = 32 * t + 8 * (r >> 2) + h4 + (r & 3);
+        S[t][r] = kk < lim ? S[t][r] : -INFINITY;
+      }
+  };
+  // Slow path for the current block (its missing keys already masked): move m to
   // the row max where the block left the fast path's range (both lanes of a
   // row agree), rescale O and the sum, redo P. Rows whose running sum is
   // negligible drop it (it holds no information relative to the new m)
   // instead of scaling it up.
-  auto slow = [&](floatx16 (&S)[2], u32x4 (&pb)[4], int lim) {
-    if (lim < kBlockK) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
-          S[t][r] = kk < lim ? S[t][r] : -INFINITY;
-        }
-    }
+  auto slow = [&](floatx16 (&S)[2], u32x4 (&pb)[4]) {
     float mx = S[0][0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) mx = fmaxf(mx, S[0][r]);
@@ -361,6 +366,11 @@ void bsattn_fwd_kernel(const AttnParams p) {
       }
     }
 
+    // keys past the sequence end (partial or out-of-range blocks) are masked
+    // before the exponentials, so such a block stays on the fast path unless
+    // its sums leave the range
+    const int lim = valid_keys(cur);
+    if (lim < kBlockK) mask_keys(S, lim);
     u32x4 pb[4];
     float bs = exp_block(S, pb);  // changes no state: a skipped block drops it
     if constexpr (kPv) {
@@ -374,8 +384,7 @@ void bsattn_fwd_kernel(const AttnParams p) {
           p.pv_map[((bh * p.nqb + qb) * 4 + w) * p.pv_w + cur] = 1;
       }
     }
-    const int lim = valid_keys(cur);
-    if (__ballot(!(bs <= kHigh) || !(ls + bs >= kLow)) || lim < kBlockK) bs = slow(S, pb, lim);
+    if (__ballot(!(bs <= kHigh) || !(ls + bs >= kLow))) bs = slow(S, pb);
     ls += bs;
 
     u32x4 va[4][2];  // all Vt operands of the block, read before the first product
