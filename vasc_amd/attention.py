@@ -131,7 +131,8 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
     attn_pooled = predict_attention(q_patch, k_re[:, :, :n_patch], pool_mode=pool_mode)
     x_patch, x_special, sparsity = sparse_global_attention(
         q_patch, q_special, k_re, v_re, attn_pooled, sparse_ratio=sparse_ratio, cdf_threshold=cdf_threshold,
-        layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch, **research)
+        layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch,
+        want_sparsity=aux_output_store is not None, **research)
     if aux_output_store is not None:
         aux_output_store["sparsity"] = sparsity
     out = ops.restore_tokens(x_patch, x_special, N, P, S)

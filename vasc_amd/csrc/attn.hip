@@ -155,6 +155,9 @@ void bsattn_fwd_kernel(const AttnParams p) {
   const int64_t o_sb = sp ? p.o2_sb : p.o_sb, o_sh = sp ? p.o2_sh : p.o_sh, o_st = sp ? p.o2_st : p.o_st;
   const int64_t qrow = static_cast<int64_t>(qb) * kBlockQ + w * 32 + lr;
   const bool qvalid = qrow < nq;
+  // a wave whose 32 rows all lie past the queries (the short last block of
+  // the special queries) only stages its share of the tiles
+  const bool idle = static_cast<int64_t>(qb) * kBlockQ + w * 32 >= nq;
   uint16_t *optr = odst + b * o_sb + h * o_sh + (qvalid ? qrow : 0) * o_st;
 
   if (n == 0) {
@@ -322,6 +325,7 @@ void bsattn_fwd_kernel(const AttnParams p) {
     }
     const uint16_t *ks = smem[buf][0];
     const uint16_t *vs = smem[buf][1];
+    if (!kPv && idle) return;
 
     // S^T tiles: keys 32t + [0,32) x this wave's 32 query rows.
     floatx16 S[2];

@@ -557,12 +557,13 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
                             value: torch.Tensor, pooled_score: torch.Tensor, *, sparse_ratio: float | None = None,
                             topk: int | None = None, cdf_threshold: float | None = None, layer_idx: int = 0,
                             routing_stats_store: dict | None = None, routing_state: dict | None = None,
-                            num_patch_tokens: int | None = None, **research):
+                            num_patch_tokens: int | None = None, want_sparsity: bool = True, **research):
     """``block_sparse_attn_cuda`` for a whole global layer: the selection of
     the patch queries as there, and the special-token queries (which the
     reference runs through a dense SDPA, ATT:8464-8484) over every key in
     the same attention launch. Returns ``(o_patch, o_special, sparsity)``
-    in bf16 (``o_special`` None without special queries)."""
+    in bf16 (``o_special`` None without special queries; ``sparsity`` None
+    unless ``want_sparsity``)."""
     _require_gpu(q_patch, "query")
     sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
                                         routing_stats_store, routing_state, num_patch_tokens, research)
@@ -575,4 +576,4 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
         o_patch, pv_map = ops.block_sparse_attn_pv(q_patch, key, vt, sel["index"], sel["count"], thr)
         o_special = None if q_special is None else ops.dense_attn(q_special, key, vt)
         _record_pv_execution(routing_state, pv_map, pooled_score.shape[-1])
-    return o_patch, o_special, _sparsity(sel, total_kblk)
+    return o_patch, o_special, (_sparsity(sel, total_kblk) if want_sparsity else None)
