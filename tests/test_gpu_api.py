@@ -132,6 +132,8 @@ def test_cosa_mask_api_chain_bit_exact(release_env):
         assert np.array_equal(_bits(st_gpu[SW.STATE_KEY]), np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
         assert np.array_equal(_bits(st_gpu[SW.PENDING_KEY]), st_ref[OS.PENDING_KEY].view(np.uint32))
         assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_priority"]), info["priority"].view(np.uint32))
+        assert np.array_equal(st_gpu["cosa_value_risk_pair_qk_order_priority"].cpu().numpy(),
+                              np.asarray(st_ref["cosa_value_risk_pair_qk_order_priority"], np.float32))
     t_gpu = SW.finalize_cosa_value_risk_pair_debt(st_gpu)
     t_ref = OS.finalize(st_ref)
     assert t_gpu and t_ref and SW.finalize_cosa_value_risk_pair_debt(st_gpu) == {}

@@ -59,3 +59,21 @@ def test_pi3_odd_layers_are_global_with_logical_index():
     with pytest.raises(ValueError):
         install.sparse_model_from_pi3(Pi3Decoder(dim=128, depth=6, num_heads=2), sparse_ratio=0.5,
                                       layer_sparsity_ratios=[0.5] * 2, verbose=False)
+
+
+def test_patch_tokens_equal_the_convolution():
+    """The runners' patch embedding as one GEMM over non-overlapping patches
+    equals the strided convolution (ragged borders dropped as the conv does);
+    other convolutions fall back to the module itself."""
+    import torch
+
+    from vasc_amd.aggregator import patch_tokens
+    torch.manual_seed(0)
+    x = torch.randn(3, 3, 70, 85)
+    conv = torch.nn.Conv2d(3, 32, 14, 14)
+    ref = conv(x).flatten(2).transpose(1, 2)
+    got = patch_tokens(conv, x)
+    assert got.shape == ref.shape == (3, 30, 32)
+    assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5)
+    overlap = torch.nn.Conv2d(3, 8, 4, 2)
+    assert torch.equal(patch_tokens(overlap, x), overlap(x).flatten(2).transpose(1, 2))

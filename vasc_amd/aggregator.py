@@ -194,6 +194,22 @@ def _ln(norm: nn.LayerNorm):
     return (norm.weight, norm.bias, norm.eps)
 
 
+def patch_tokens(conv: nn.Conv2d, x: torch.Tensor) -> torch.Tensor:
+    """``conv(x).flatten(2).transpose(1, 2)`` for the patch embedding: a
+    convolution whose stride equals its kernel (no padding, dilation or
+    groups) is one GEMM over the non-overlapping patches, which hipBLASLt
+    runs far faster than the library's im2col path for a 3-channel input."""
+    p = conv.kernel_size
+    if not (conv.stride == p and conv.padding == (0, 0) and conv.dilation == (1, 1) and conv.groups == 1):
+        return conv(x).flatten(2).transpose(1, 2)
+    BN, C, Hi, Wi = x.shape
+    h, w = Hi // p[0], Wi // p[1]
+    x = x[:, :, :h * p[0], :w * p[1]]
+    patches = x.reshape(BN, C, h, p[0], w, p[1]).permute(0, 2, 4, 1, 3, 5).reshape(BN * h * w, C * p[0] * p[1])
+    out = nn.functional.linear(patches, conv.weight.reshape(conv.out_channels, -1), conv.bias)
+    return out.view(BN, h * w, conv.out_channels)
+
+
 def grid_positions(frames: int, h: int, w: int, special: int, device) -> torch.Tensor:
     """``[frames, special + h*w, 2]`` integer (row, column) positions: patch
     tokens get ``(y+1, x+1)``, special tokens ``(0, 0)`` (vggt.py:122-131)."""
@@ -243,7 +259,7 @@ class Aggregator(nn.Module):
             routing_state.clear()
         B, N, _, Hi, Wi = images.shape
         x = ((images - self._resnet_mean) / self._resnet_std).view(B * N, 3, Hi, Wi).to(self.patch_embed.weight.dtype)
-        tokens = self.patch_embed(x).flatten(2).transpose(1, 2)
+        tokens = patch_tokens(self.patch_embed, x)
         special = [self._expand(self.register_token, B, N)]
         if self.camera_token is not None:
             special.insert(0, self._expand(self.camera_token, B, N))
@@ -291,7 +307,7 @@ class Pi3Decoder(nn.Module):
         """images ``[B, N, 3, H, W]`` -> (concatenated last two outputs, positions)."""
         B, N, _, Hi, Wi = images.shape
         x = images.view(B * N, 3, Hi, Wi).to(self.patch_embed.weight.dtype)
-        hidden = self.patch_embed(x).flatten(2).transpose(1, 2)
+        hidden = patch_tokens(self.patch_embed, x)
         return self.decode(hidden, N, Hi, Wi)
 
     def decode(self, hidden: torch.Tensor, N: int, H: int, W: int):

@@ -192,7 +192,9 @@ def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_i
         routing_state["cosa_value_risk_pair_priority"] = out["priority"]
     routing_state["cosa_value_risk_pair_max_patch_blocks"] = int(M)
     routing_state["cosa_value_risk_pair_selected_indices"] = out["index"][..., :M]
-    routing_state["cosa_value_risk_pair_qk_order_priority"] = score.float().clamp_min(0.0).nan_to_num(nan=0.0)
+    # clamp_min(0) then NaN -> 0, as the reference's score (SW:3680-3684), in one pass
+    sf = score.float()
+    routing_state["cosa_value_risk_pair_qk_order_priority"] = torch.where(sf > 0, sf, 0.0)
 
 
 def _pv_execution_service(pv_map: torch.Tensor, patch_blocks: int) -> torch.Tensor:
