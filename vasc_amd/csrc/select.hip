@@ -484,7 +484,8 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
   float refl_pp = 0.f, sig_pp = 0.f, d_pp = 0.f;
   if (has) {
     const double *part = p.part + bh * p.nchunks * p.P + pp;
-#pragma unroll 8
+    // 32 loads in flight per batch (C3 has 33 chunks); the sum keeps its order
+#pragma unroll 32
     for (int64_t c = 0; c < p.nchunks; ++c) acc_pp = acc_pp + part[c * p.P];
     d_pp = settle_one(p, bh * p.P + pp, &refl_pp, &sig_pp);
   }
@@ -492,9 +493,9 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
     double acc = 0.0, dacc = 0.0, useful = 0.0, wasted = 0.0, consumed = 0.0;
     // unrolled so several iterations' loads are in flight; the float64 chains
     // keep their order
-#pragma unroll 4
+#pragma unroll 16
     for (int64_t q = tid; q < p.Q; q += 64) acc = acc + static_cast<double>(p.rowpair[bh * p.Q + q]);
-#pragma unroll 4
+#pragma unroll 8
     for (int64_t j = tid; j < p.P; j += 64) {
       float refl, sig;
       const float d = settle_one(p, bh * p.P + j, &refl, &sig);
