@@ -19,10 +19,10 @@
 // Eight lanes own one (token, tensor, head) row of 64 features, 8 per lane,
 // so a row is one 128-byte segment on both sides; the LayerNorm sums are
 // xor butterflies inside the 8-lane group and the rotary partner of a
-// feature (16 places away inside its half) sits two lanes away. A
-// workgroup takes 64 tokens of one tensor and head (index arithmetic in 32
-// bits, tensor and head scalar), and issues both of a lane's loads before
-// it uses the first.
+// feature (16 places away inside its half) sits two lanes away. A pack
+// workgroup takes 128 tokens of one tensor and head (a restore workgroup 64;
+// index arithmetic in 32 bits, tensor and head scalar), and issues all of a
+// lane's loads before it uses the first.
 // Precedent in the reference: kernels/qkv_layout.py:8-157 (layout only).
 #include "common.h"
 
@@ -32,7 +32,11 @@ namespace {
 constexpr int kHeadDim = 64;
 constexpr int kThreads = 256;
 constexpr int kRows = kThreads / 8;  // token rows per pass: 8 lanes per 64-feature row
-constexpr int kPasses = 2;           // token rows per lane group
+// token rows per lane group: the pack kernel's per-row norm and rotary work
+// hides behind four rows' loads; the copy-only restore does best with two
+constexpr int kPackPasses = 4;
+constexpr int kPackTokens = kRows * kPackPasses;
+constexpr int kPasses = 2;
 constexpr int kTokens = kRows * kPasses;
 
 struct PackParams {
@@ -51,11 +55,11 @@ struct PackParams {
 
 
 // Workgroup (x, b): tensor/head th = x % 3H (0..H-1 q, H..2H-1 k, 2H..3H-1
-// v), tokens [64 (x / 3H), +64) of batch entry b; consecutive workgroups
+// v), tokens [128 (x / 3H), +128) of batch entry b; consecutive workgroups
 // take the heads of the same tokens. Lane group g (8 lanes, 8 features
-// each) handles tokens g and g + 32 of the block. Every load (features,
-// positions, then the rotary table entries) is issued before the first
-// result is computed.
+// each) handles tokens g, g + 32, g + 64 and g + 96 of the block. Every load
+// (features, positions, then the rotary table entries) is issued before the
+// first result is computed.
 __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) {
   const int32_t H = p.H, T = p.N * p.P;
   const int32_t th = static_cast<int32_t>(blockIdx.x % (3 * H));
@@ -66,22 +70,22 @@ __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) 
   const bool norm = part < 2 && p.norm[part];
   const bool rope = part < 2 && p.pos;
   const uint16_t *src = p.src[part] + b * p.sb[part] + h * p.sh[part] + sub * 8;
-  int32_t t[kPasses];
-  bool ok[kPasses];
-  u32x4 raw[kPasses];
-  int32_t pq[kPasses];
+  int32_t t[kPackPasses];
+  bool ok[kPackPasses];
+  u32x4 raw[kPackPasses];
+  int32_t pq[kPackPasses];
 #pragma unroll
-  for (int i = 0; i < kPasses; ++i) {
-    t[i] = tb * kTokens + i * kRows + (tid >> 3);
+  for (int i = 0; i < kPackPasses; ++i) {
+    t[i] = tb * kPackTokens + i * kRows + (tid >> 3);
     ok[i] = t[i] < T;
     const int32_t tc = ok[i] ? t[i] : T - 1;  // in-bounds stand-in for rows past the end
     raw[i] = *reinterpret_cast<const u32x4 *>(src + static_cast<int64_t>(tc) * p.st[part]);
     pq[i] = rope ? p.pos[b * p.pos_sb + static_cast<int64_t>(tc) * p.pos_st + (sub >> 2)] : 0;
   }
-  float cs[kPasses][8], sn[kPasses][8];
+  float cs[kPackPasses][8], sn[kPackPasses][8];
   if (rope) {
 #pragma unroll
-    for (int i = 0; i < kPasses; ++i) {
+    for (int i = 0; i < kPackPasses; ++i) {
       const int32_t q = pq[i] < 0 ? 0 : (pq[i] >= p.rope_n ? p.rope_n - 1 : pq[i]);
       const floatx4 *c4 = reinterpret_cast<const floatx4 *>(p.rope_cos + q * 16 + (sub & 1) * 8);
       const floatx4 *s4 = reinterpret_cast<const floatx4 *>(p.rope_sin + q * 16 + (sub & 1) * 8);
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) 
   const int32_t np = p.N * (p.P - p.S), ns = p.N * p.S;
   const int64_t bh = b * H + h;
 #pragma unroll
-  for (int i = 0; i < kPasses; ++i) {
+  for (int i = 0; i < kPackPasses; ++i) {
     float x[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -210,7 +214,7 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   VASC_REQUIRE(B > 0 && H > 0 && N > 0 && P > 0 && S >= 0 && S <= P, "invalid sizes B=%lld H=%lld N=%lld P=%lld S=%lld",
                (long long)B, (long long)H, (long long)N, (long long)P, (long long)S);
   VASC_REQUIRE(B < 65536 && H < 4096 && N * P < (int64_t(1) << 31) / 64, "too many tokens or heads");
-  VASC_REQUIRE(cdiv(N * P, kTokens) * 3 * H < (int64_t(1) << 31), "grid too large");
+  VASC_REQUIRE(cdiv(N * P, kPackTokens) * 3 * H < (int64_t(1) << 31), "grid too large");
   int rc;
   if ((rc = check_src("q", q, q_sb, q_st, q_sh))) return rc;
   if ((rc = check_src("k", k, k_sb, k_st, k_sh))) return rc;
@@ -242,7 +246,7 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   p.rope_cos = rope_cos; p.rope_sin = rope_sin;
   p.rope_n = static_cast<int32_t>(rope_n < (int64_t(1) << 30) ? rope_n : (int64_t(1) << 30));
   p.q_patch = q_patch; p.q_special = q_special; p.k_out = k_out; p.v_out = v_out;
-  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(cdiv(N * P, kTokens) * 3 * H), static_cast<unsigned>(B)),
+  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(cdiv(N * P, kPackTokens) * 3 * H), static_cast<unsigned>(B)),
                      dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
   return check_launch("vasc_pack_qkv");
 }
