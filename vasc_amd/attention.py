@@ -105,6 +105,7 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
     one kernel restores the frame-major order before ``proj`` (ATT:8992-9030).
     """
     from .aggregator import fused_layout_supported, layer_norm_args
+    from .launcher import routing_config
     from .sparse_wrapper import sparse_global_attention
 
     if routing_state is None:
@@ -128,11 +129,18 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
         q_patch, q_special, k_re, v_re = ops.pack_qkv(
             *(t.to(torch.bfloat16).transpose(1, 2) for t in (q, k, v)), N, P, S)
     n_patch = N * (P - S)
-    attn_pooled = predict_attention(q_patch, k_re[:, :, :n_patch], pool_mode=pool_mode)
+    innovation = None
+    if pool_mode == "avg" and routing_config().mode == "vasc":
+        # Q, K and V pooled in one pass: predict_attention's pooled Q/K and
+        # the selector's value innovation
+        pq, pk, _, innovation = ops.pool_qkv(q_patch, k_re[:, :, :n_patch], v_re[:, :, :n_patch])
+        attn_pooled = ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(hd))
+    else:
+        attn_pooled = predict_attention(q_patch, k_re[:, :, :n_patch], pool_mode=pool_mode)
     x_patch, x_special, sparsity = sparse_global_attention(
         q_patch, q_special, k_re, v_re, attn_pooled, sparse_ratio=sparse_ratio, cdf_threshold=cdf_threshold,
         layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch,
-        want_sparsity=aux_output_store is not None, **research)
+        want_sparsity=aux_output_store is not None, _innovation=innovation, **research)
     if aux_output_store is not None:
         aux_output_store["sparsity"] = sparsity
     out = ops.restore_tokens(x_patch, x_special, N, P, S)

@@ -441,10 +441,11 @@ def _check_research_kwargs(kwargs: dict) -> None:
 
 def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torch.Tensor, topk, sparse_ratio,
                       cdf_threshold, layer_idx: int, routing_stats_store, routing_state, num_patch_tokens,
-                      research: dict):
+                      research: dict, innovation: torch.Tensor | None = None):
     """Mode switch, budget, mixed-tail and sink rules and kernel 2 of
     block_sparse_attn_cuda (SW:6998-7041, 7559-7770). Returns the selection
-    and the total key-block count."""
+    and the total key-block count. ``innovation``: the pair innovation of
+    the patch values when the caller pooled them already."""
     _check_research_kwargs(research)
     for t, name in ((key, "key"), (value, "value"), (pooled_score, "pooled_score")):
         _require_gpu(t, name)
@@ -469,7 +470,8 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
             raise ValueError("CoSA pair debt requires routing_state")
         B, H = pooled_score.shape[:2]
         P = (orig_kblk + 1) // 2
-        _, _, _, innovation = ops.pool_qkv(v=value[..., :num_patch_tokens, :])
+        if innovation is None:
+            _, _, _, innovation = ops.pool_qkv(v=value[..., :num_patch_tokens, :])
         if base is not None:
             # no hint with a cdf threshold: M is the largest row capacity (SW:3709-3712)
             hint = int(base.max())
@@ -559,16 +561,19 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
                             value: torch.Tensor, pooled_score: torch.Tensor, *, sparse_ratio: float | None = None,
                             topk: int | None = None, cdf_threshold: float | None = None, layer_idx: int = 0,
                             routing_stats_store: dict | None = None, routing_state: dict | None = None,
-                            num_patch_tokens: int | None = None, want_sparsity: bool = True, **research):
+                            num_patch_tokens: int | None = None, want_sparsity: bool = True,
+                            _innovation: torch.Tensor | None = None, **research):
     """``block_sparse_attn_cuda`` for a whole global layer: the selection of
     the patch queries as there, and the special-token queries (which the
     reference runs through a dense SDPA, ATT:8464-8484) over every key in
     the same attention launch. Returns ``(o_patch, o_special, sparsity)``
     in bf16 (``o_special`` None without special queries; ``sparsity`` None
-    unless ``want_sparsity``)."""
+    unless ``want_sparsity``; ``_innovation``: the patch values' pair
+    innovation when the caller pooled them with Q and K)."""
     _require_gpu(q_patch, "query")
     sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
-                                        routing_stats_store, routing_state, num_patch_tokens, research)
+                                        routing_stats_store, routing_state, num_patch_tokens, research,
+                                        innovation=_innovation)
     vt = ops.pack_v(value)
     thr = _pv_threshold(key, layer_idx)
     if thr is None:
