@@ -268,9 +268,12 @@ def run_c5(dev) -> int:
 
 
 class AttnLaunchEvents:
-    """hipEvents around every ``ops.global_attn`` launch (the sparse global
-    layers' attention kernel) on the stream it is launched on, plus the
-    lists of each layer's latest launch for its algorithmic flops."""
+    """hipEvents around every ``ops.global_attn`` / ``ops.global_attn_tokens``
+    launch (the sparse global layers' attention kernel) on the stream it is
+    launched on, plus the lists of each layer's latest launch for its
+    algorithmic flops."""
+
+    _NAMES = ("global_attn", "global_attn_tokens")
 
     def __init__(self, layers: int):
         self.layers = layers
@@ -278,29 +281,32 @@ class AttnLaunchEvents:
         self.lists: dict = {}
         self.enabled = False
 
-    def __enter__(self):
-        from vasc_amd import ops
-        self._ops = ops
-        self._orig = ops.global_attn
-
-        def timed(q_patch, q_special, k, vt, index, count, **kw):
+    def _wrap(self, orig):
+        def timed(q_patch, q_special, k, vt, index, count, *args, **kw):
             if not self.enabled:
-                return self._orig(q_patch, q_special, k, vt, index, count, **kw)
+                return orig(q_patch, q_special, k, vt, index, count, *args, **kw)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            out = self._orig(q_patch, q_special, k, vt, index, count, **kw)
+            out = orig(q_patch, q_special, k, vt, index, count, *args, **kw)
             b.record()
             self.events.append((a, b))
             n_special = 0 if q_special is None else q_special.shape[2]
             self.lists[len(self.events) % self.layers] = (index, count, q_patch.shape[2], k.shape[2], n_special,
                                                           q_patch.shape[1], q_patch.shape[3])
             return out
+        return timed
 
-        ops.global_attn = timed
+    def __enter__(self):
+        from vasc_amd import ops
+        self._ops = ops
+        self._orig = {name: getattr(ops, name) for name in self._NAMES}
+        for name, fn in self._orig.items():
+            setattr(ops, name, self._wrap(fn))
         return self
 
     def __exit__(self, *exc):
-        self._ops.global_attn = self._orig
+        for name, fn in self._orig.items():
+            setattr(self._ops, name, fn)
 
     def mean_ms(self) -> float:
         return statistics.fmean(a.elapsed_time(b) for a, b in self.events)
@@ -891,7 +897,7 @@ def main() -> int:
         "speedup_global_layer_vs_dense": agg["speedup_global_layers_vs_dense"],
         "aggregator": agg,
         "roofline": {
-            "kernel": "bsattn_fwd_kernel (vasc_global_attn_fwd: patch queries over their lists + special queries)",
+            "kernel": "bsattn_fwd_kernel (vasc_global_attn_tokens_fwd: patch queries over their lists + special queries, results on the frame-major token rows)",
             "bound": "mfma",
             "achieved": achieved,
             "peak": PEAK_BF16_TFLOPS,

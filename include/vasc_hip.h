@@ -331,6 +331,29 @@ int vasc_global_attn_fwd(const uint16_t *q_patch, int64_t qp_sb, int64_t qp_sh,
                          const int32_t *block_count, float sm_scale,
                          void *stream);
 
+/*
+ * vasc_global_attn_fwd writing the layer's output order: the patch and
+ * special query results go straight to their frame-major token rows of out
+ * [B, N*P, H*d] (contiguous), the tensor the layer's restore to frame-major
+ * order and transpose before the output projection produce
+ * (attention.py:8992-9027, tokens.py:64-126): patch query i of frame
+ * n = i / (P-S) to token n*P + S + i % (P-S), special query j to token
+ * (j / S)*P + j % S. n_patch = N*(P-S), n_special = N*S, nk = N*P.
+ * Built variant: d == 64.
+ */
+int vasc_global_attn_tokens_fwd(const uint16_t *q_patch, int64_t qp_sb,
+                                int64_t qp_sh, int64_t qp_st,
+                                const uint16_t *q_special, int64_t qs_sb,
+                                int64_t qs_sh, int64_t qs_st,
+                                const uint16_t *k, int64_t k_sb, int64_t k_sh,
+                                int64_t k_st, const uint16_t *vt,
+                                uint16_t *out, int64_t B, int64_t H, int64_t N,
+                                int64_t P, int64_t S, int64_t nk, int64_t d,
+                                const int32_t *block_index,
+                                int64_t index_width,
+                                const int32_t *block_count, float sm_scale,
+                                void *stream);
+
 /* Dense variant of kernel 4: every query block attends to all key blocks. */
 int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
                         int64_t q_st, const uint16_t *k, int64_t k_sb,

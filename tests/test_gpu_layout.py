@@ -127,6 +127,34 @@ def test_global_attn_patch_and_special_in_one_launch():
     assert none is None and np.array_equal(_bits(o_p2), _bits(o_p))
 
 
+@pytest.mark.parametrize("N,P,S,H", [(3, 1041, 5, 2), (4, 70, 0, 1), (2, 7, 7 - 1, 2)])
+def test_global_attn_tokens_equals_attention_then_restore(N, P, S, H):
+    """vasc_global_attn_tokens_fwd writes every result on its frame-major
+    token row: bit-identical to vasc_global_attn_fwd followed by the restore
+    kernel (frames with and without special tokens, a ragged last block)."""
+    from vasc_amd import ops
+    B, D = 1, 64
+    Np, Ns, Tk = N * (P - S), N * S, N * P
+    q = _bf16((B, H, Np, D), 31).cuda()
+    qs = _bf16((B, H, Ns, D), 32).cuda() if S else None
+    k = _bf16((B, H, Tk, D), 33).cuda()
+    v = _bf16((B, H, Tk, D), 34).cuda()
+    nkb, qb = math.ceil(Tk / 64), math.ceil(Np / 128)
+    rng = np.random.default_rng(35)
+    idx = np.full((B, H, qb, nkb), -1, np.int32)
+    cnt = rng.integers(1, nkb + 1, size=(B, H, qb)).astype(np.int32)
+    for h in range(H):
+        for i in range(qb):
+            idx[0, h, i, : cnt[0, h, i]] = np.sort(rng.choice(nkb, cnt[0, h, i], replace=False))
+    index, count = torch.from_numpy(idx).cuda(), torch.from_numpy(cnt).cuda()
+    vt = ops.pack_v(v)
+    o_p, o_s = ops.global_attn(q, qs, k, vt, index, count)
+    ref = ops.restore_tokens(o_p, o_s, N, P, S)
+    got = ops.global_attn_tokens(q, qs, k, vt, index, count, N, P, S)
+    assert got.shape == (B, Tk, H * D)
+    assert np.array_equal(_bits(got), _bits(ref))
+
+
 def test_global_layer_sparse_matches_oracle_layer():
     """The fused layer forward (layout kernel with LayerNorm + rotary, pooled
     predictor, Top-K selection, one attention launch, restore) against the

@@ -158,6 +158,13 @@ def test_host_only_queries_and_argument_errors():
     rc = lib.vasc_block_sparse_attn_pv_fwd(None, 0, 0, 8, None, 0, 0, 8, None, None, 0, 0, 8, 1, 1, 128, 64, 64,
                                            None, 1, None, 0, ctypes.c_float(0.125), None, None, None)
     assert rc == 1 and b"pv_threshold" in lib.vasc_last_error()
+    # token-major global attention: frame sizes and the key count are checked first
+    rc = lib.vasc_global_attn_tokens_fwd(fake, 0, 0, 8, fake, 0, 0, 8, fake, 0, 0, 8, fake, fake, 1, 1, 2, 5, 5,
+                                         10, 64, fake, 1, fake, f(0.125), None)
+    assert rc == 1 and b"frame sizes" in lib.vasc_last_error()
+    rc = lib.vasc_global_attn_tokens_fwd(fake, 0, 0, 8, fake, 0, 0, 8, fake, 0, 0, 8, fake, fake, 1, 1, 2, 6, 1,
+                                         10, 64, fake, 1, fake, f(0.125), None)
+    assert rc == 1 and b"N*P" in lib.vasc_last_error()
     # runner op: built widths, required rows, outputs and alignment
     rc = lib.vasc_residual_norm(fake, 1000, fake, 1000, None, None, None, f(1e-6), fake, 1000, None, 0, 4, 1000, None)
     assert rc == 2 and b"not built" in lib.vasc_last_error()

@@ -55,6 +55,8 @@ SIGNATURES: dict[str, tuple] = {
     "vasc_global_attn_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64, P,
                                        P, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64, I64, I64,
                                        P, I64, P, c_float, P]),
+    "vasc_global_attn_tokens_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64, P, P,
+                                              I64, I64, I64, I64, I64, I64, I64, P, I64, P, c_float, P]),
     "vasc_pack_qkv": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64,
                                 I64, I64, I64, I64, I64, I64, P, P, c_float, I32, P, P, c_float, I32,
                                 P, I64, I64, P, P, I64, P, P, P, P, P]),

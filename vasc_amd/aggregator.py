@@ -102,8 +102,9 @@ class Attention(nn.Module):
                                    q_norm=layer_norm_args(self.q_norm), k_norm=layer_norm_args(self.k_norm),
                                    pos=pos if self.rope is not None else None,
                                    rope_tables=self._tables(pos, D, x.device))
-        o = ops.dense_attn(qp, k, ops.pack_v(v), scale=1.0 / math.sqrt(D))
-        out = ops.restore_tokens(o, None, 1, T, 0)
+        # the kernel writes straight into the frame-major [B, T, H*D] rows proj reads
+        out = torch.empty(B, T, H * D, device=x.device, dtype=torch.bfloat16)
+        ops.dense_attn(qp, k, ops.pack_v(v), scale=1.0 / math.sqrt(D), out=out.view(B, T, H, D).transpose(1, 2))
         return self.proj_drop(self.proj(out.to(x.dtype)))
 
     def _tables(self, pos, head_dim, device):

@@ -102,7 +102,9 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
     LayerNorms (or identities) and the rope is ``RotaryPositionEmbedding2D``;
     other modules run their norms and rope in torch first. Special-token
     queries attend to every key in the same launch as the patch queries, and
-    one kernel restores the frame-major order before ``proj`` (ATT:8992-9030).
+    that launch writes every result on its frame-major token row, the order
+    ``proj`` reads (the reference's restore and transpose, ATT:8992-9030).
+    With a PV post-cut the separate restore kernel does that step.
     """
     from .aggregator import fused_layout_supported, layer_norm_args
     from .launcher import routing_config
@@ -137,13 +139,12 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
         attn_pooled = ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(hd))
     else:
         attn_pooled = predict_attention(q_patch, k_re[:, :, :n_patch], pool_mode=pool_mode)
-    x_patch, x_special, sparsity = sparse_global_attention(
+    x_patch, _, sparsity = sparse_global_attention(
         q_patch, q_special, k_re, v_re, attn_pooled, sparse_ratio=sparse_ratio, cdf_threshold=cdf_threshold,
         layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch,
-        want_sparsity=aux_output_store is not None, _innovation=innovation, **research)
+        want_sparsity=aux_output_store is not None, _innovation=innovation, token_layout=(N, P, S), **research)
     if aux_output_store is not None:
         aux_output_store["sparsity"] = sparsity
-    out = ops.restore_tokens(x_patch, x_special, N, P, S)
-    out = self.proj(out.to(x.dtype))
+    out = self.proj(x_patch.to(x.dtype))  # already in frame-major token order
     drop = getattr(self, "proj_drop", None)
     return drop(out) if drop is not None else out

@@ -77,6 +77,9 @@ struct AttnParams {
   uint16_t *o2;
   int64_t o2_sb, o2_sh, o2_st;
   int64_t nq2, nq2b, num_wg2;
+  // token-major output (tok_p > 0): query rows land on the frame-major token
+  // rows of o (frames of tok_p tokens, tok_s special ones first)
+  int64_t tok_p, tok_s;
   // PV post-cut (kPv instances): per-head thresholds in log2 units and the
   // per-wave execution map [B, H, nqb * 4, pv_w] (written where PV ran)
   const float *pv_thr;
@@ -158,7 +161,12 @@ void bsattn_fwd_kernel(const AttnParams p) {
   // a wave whose 32 rows all lie past the queries (the short last block of
   // the special queries) only stages its share of the tiles
   const bool idle = static_cast<int64_t>(qb) * kBlockQ + w * 32 >= nq;
-  uint16_t *optr = odst + b * o_sb + h * o_sh + (qvalid ? qrow : 0) * o_st;
+  int64_t orow = qvalid ? qrow : 0;
+  if (p.tok_p > 0) {
+    const int64_t per = sp ? p.tok_s : p.tok_p - p.tok_s;  // queries per frame of this kind
+    orow = (orow / per) * p.tok_p + (sp ? 0 : p.tok_s) + orow % per;
+  }
+  uint16_t *optr = odst + b * o_sb + h * o_sh + orow * o_st;
 
   if (n == 0) {
     if (qvalid) {
@@ -437,6 +445,11 @@ int check_bhtd(const char *name, const void *ptr, int64_t sb, int64_t sh, int64_
   return VASC_OK;
 }
 
+// Token-major output of vasc_global_attn_tokens_fwd (absent: P == 0).
+struct OutTokens {
+  int64_t P = 0, S = 0;
+};
+
 // Special-token queries of vasc_global_attn_fwd (absent: q2 == NULL).
 struct SpecialQueries {
   const uint16_t *q2 = nullptr;
@@ -452,7 +465,7 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
                 int64_t nq, int64_t nk, int64_t d, const int32_t *idx, int64_t idx_w,
                 const int32_t *cnt, int32_t delta, float sm_scale, void *stream,
                 const SpecialQueries &sq = SpecialQueries(), const float *pv_thr = nullptr,
-                int32_t *pv_map = nullptr) {
+                int32_t *pv_map = nullptr, const OutTokens &ot = OutTokens()) {
   VASC_SUPPORTED(d == kHeadDim, "head_dim %lld not built (built: 64)", (long long)d);
   VASC_REQUIRE(B > 0 && H > 0 && nq > 0 && nk > 0, "sizes must be positive");
   int rc;
@@ -487,6 +500,8 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
   p.pv_thr = pv_thr;
   p.pv_map = pv_map;
   p.pv_w = p.nkb;
+  p.tok_p = ot.P;
+  p.tok_s = ot.S;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   auto kern = dense ? bsattn_fwd_kernel<true> : (pv_thr ? bsattn_fwd_kernel<false, true> : bsattn_fwd_kernel<false>);
   hipLaunchKernelGGL(kern, dim3(p.num_wg + p.num_wg2), dim3(kThreads), 0, s, p);
@@ -551,4 +566,34 @@ extern "C" int vasc_global_attn_fwd(const uint16_t *q_patch, int64_t qp_sb, int6
   VASC_REQUIRE(n_special >= 0, "n_special must be non-negative");
   return launch_attn(false, q_patch, qp_sb, qp_sh, qp_st, k, k_sb, k_sh, k_st, vt, o_patch, op_sb, op_sh, op_st,
                      B, H, n_patch, nk, d, block_index, index_width, block_count, 0, sm_scale, stream, sq);
+}
+
+extern "C" int vasc_global_attn_tokens_fwd(const uint16_t *q_patch, int64_t qp_sb, int64_t qp_sh, int64_t qp_st,
+                                           const uint16_t *q_special, int64_t qs_sb, int64_t qs_sh, int64_t qs_st,
+                                           const uint16_t *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                           const uint16_t *vt, uint16_t *out, int64_t B, int64_t H, int64_t N,
+                                           int64_t P, int64_t S, int64_t nk, int64_t d,
+                                           const int32_t *block_index, int64_t index_width,
+                                           const int32_t *block_count, float sm_scale, void *stream) {
+  using namespace vasc;
+  VASC_REQUIRE(N > 0 && P > S && S >= 0, "invalid frame sizes N=%lld P=%lld S=%lld", (long long)N, (long long)P,
+               (long long)S);
+  VASC_REQUIRE(nk == N * P, "nk %lld must be N*P = %lld", (long long)nk, (long long)(N * P));
+  VASC_REQUIRE(out != nullptr && (reinterpret_cast<uintptr_t>(out) & 15) == 0, "out must be a 16-byte aligned [B,N*P,H*d]");
+  // out [B, N*P, H*d] contiguous: (b, h, token) strides
+  const int64_t o_sb = N * P * H * d, o_sh = d, o_st = H * d;
+  SpecialQueries sq;
+  if (S > 0) {
+    int rc;
+    if ((rc = check_bhtd("q_special", q_special, qs_sb, qs_sh, qs_st))) return rc;
+    sq.q2 = q_special; sq.q2_sb = qs_sb; sq.q2_sh = qs_sh; sq.q2_st = qs_st;
+    sq.o2 = out; sq.o2_sb = o_sb; sq.o2_sh = o_sh; sq.o2_st = o_st;
+    sq.nq2 = N * S;
+  }
+  OutTokens ot;
+  ot.P = P;
+  ot.S = S;
+  return launch_attn(false, q_patch, qp_sb, qp_sh, qp_st, k, k_sb, k_sh, k_st, vt, out, o_sb, o_sh, o_st, B, H,
+                     N * (P - S), nk, d, block_index, index_width, block_count, 0, sm_scale, stream, sq, nullptr,
+                     nullptr, ot);
 }

@@ -306,6 +306,11 @@ def dense_attn(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, *, scale: flo
     nk = k.shape[2]
     if vt.shape != (B, H, math.ceil(nk / BLOCK_K), D, BLOCK_K):
         raise ValueError(f"vt shape {tuple(vt.shape)} does not match K {tuple(k.shape)}")
+    if out is not None:
+        _dev(out, "out")
+        if out.shape != (B, H, nq, D) or out.dtype != torch.bfloat16 or out.stride(3) != 1:
+            raise ValueError(f"out must be bf16 {(B, H, nq, D)} with unit stride over D, "
+                             f"got {out.dtype} {tuple(out.shape)} strides {out.stride()}")
     o = out if out is not None else torch.empty(B, H, nq, D, device=q.device, dtype=torch.bfloat16)
     scale = D ** -0.5 if scale is None else scale
     _lib.call("vasc_dense_attn_fwd", q.data_ptr(), *q.stride()[:3], k.data_ptr(), *k.stride()[:3],
@@ -345,6 +350,40 @@ def global_attn(q_patch: torch.Tensor, q_special: torch.Tensor | None, k: torch.
               *k.stride()[:3], vt.data_ptr(), o_patch.data_ptr(), *o_patch.stride()[:3], *os_args, B, H, n_patch,
               n_special, nk, D, index.data_ptr(), index.shape[-1], count.data_ptr(), float(scale), _stream())
     return o_patch, o_special
+
+
+def global_attn_tokens(q_patch: torch.Tensor, q_special: torch.Tensor | None, k: torch.Tensor, vt: torch.Tensor,
+                       index: torch.Tensor, count: torch.Tensor, frames: int, tokens_per_frame: int, special: int,
+                       *, scale: float | None = None) -> torch.Tensor:
+    """``global_attn`` followed by ``restore_tokens`` in one launch: the
+    results land on their frame-major token rows of ``[B, N*P, H*D]`` bf16."""
+    q_patch = _bhtd(q_patch, "q_patch")
+    k = _bhtd(k, "k")
+    _dev(vt, "vt")
+    B, H, n_patch, D = q_patch.shape
+    N, P, S = int(frames), int(tokens_per_frame), int(special)
+    nk = k.shape[2]
+    if n_patch != N * (P - S) or nk != N * P:
+        raise ValueError(f"q_patch/k hold {n_patch}/{nk} tokens, expected {N * (P - S)}/{N * P}")
+    if vt.shape != (B, H, math.ceil(nk / BLOCK_K), D, BLOCK_K):
+        raise ValueError(f"vt shape {tuple(vt.shape)} does not match K {tuple(k.shape)}")
+    qb = math.ceil(n_patch / BLOCK_Q)
+    index = index.to(torch.int32).contiguous()
+    count = count.to(torch.int32).contiguous()
+    if index.shape[:3] != (B, H, qb) or count.shape != (B, H, qb):
+        raise ValueError(f"index/count must be [B,H,{qb},W]/[B,H,{qb}]")
+    qs_args = (None, 0, 0, 8)
+    if S > 0:
+        if q_special is None or q_special.shape[2] != N * S:
+            raise ValueError(f"q_special must hold {N * S} tokens")
+        q_special = _bhtd(q_special, "q_special")
+        qs_args = (q_special.data_ptr(), *q_special.stride()[:3])
+    out = torch.empty(B, N * P, H * D, device=q_patch.device, dtype=torch.bfloat16)
+    scale = D ** -0.5 if scale is None else scale
+    _lib.call("vasc_global_attn_tokens_fwd", q_patch.data_ptr(), *q_patch.stride()[:3], *qs_args, k.data_ptr(),
+              *k.stride()[:3], vt.data_ptr(), out.data_ptr(), B, H, N, P, S, nk, D, index.data_ptr(),
+              index.shape[-1], count.data_ptr(), float(scale), _stream())
+    return out
 
 
 # ----------------------------------------------------------------- kernel 5

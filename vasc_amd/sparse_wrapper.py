@@ -562,14 +562,18 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
                             topk: int | None = None, cdf_threshold: float | None = None, layer_idx: int = 0,
                             routing_stats_store: dict | None = None, routing_state: dict | None = None,
                             num_patch_tokens: int | None = None, want_sparsity: bool = True,
-                            _innovation: torch.Tensor | None = None, **research):
+                            _innovation: torch.Tensor | None = None, token_layout: tuple | None = None,
+                            **research):
     """``block_sparse_attn_cuda`` for a whole global layer: the selection of
     the patch queries as there, and the special-token queries (which the
     reference runs through a dense SDPA, ATT:8464-8484) over every key in
     the same attention launch. Returns ``(o_patch, o_special, sparsity)``
     in bf16 (``o_special`` None without special queries; ``sparsity`` None
     unless ``want_sparsity``; ``_innovation``: the patch values' pair
-    innovation when the caller pooled them with Q and K)."""
+    innovation when the caller pooled them with Q and K). With
+    ``token_layout = (N, P, S)`` the first result is instead the layer's
+    frame-major ``[B, N*P, H*D]`` output (restore included) and the second
+    None."""
     _require_gpu(q_patch, "query")
     sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
                                         routing_stats_store, routing_state, num_patch_tokens, research,
@@ -577,10 +581,17 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
     vt = ops.pack_v(value)
     thr = _pv_threshold(key, layer_idx)
     if thr is None:
+        if token_layout is not None:
+            out = ops.global_attn_tokens(q_patch, q_special, key, vt, sel["index"], sel["count"], *token_layout)
+            _record_pv_execution(routing_state)
+            return out, None, (_sparsity(sel, total_kblk) if want_sparsity else None)
         o_patch, o_special = ops.global_attn(q_patch, q_special, key, vt, sel["index"], sel["count"])
         _record_pv_execution(routing_state)
     else:  # the post-cut applies to the patch queries; the special queries stay dense
         o_patch, pv_map = ops.block_sparse_attn_pv(q_patch, key, vt, sel["index"], sel["count"], thr)
         o_special = None if q_special is None else ops.dense_attn(q_special, key, vt)
         _record_pv_execution(routing_state, pv_map, pooled_score.shape[-1])
+    if token_layout is not None:
+        return ops.restore_tokens(o_patch, o_special, *token_layout), None, \
+            (_sparsity(sel, total_kblk) if want_sparsity else None)
     return o_patch, o_special, (_sparsity(sel, total_kblk) if want_sparsity else None)
