@@ -20,9 +20,11 @@
 // so a row is one 128-byte segment on both sides; the LayerNorm sums are
 // xor butterflies inside the 8-lane group and the rotary partner of a
 // feature (16 places away inside its half) sits two lanes away. A pack
-// workgroup takes 128 tokens of one tensor and head (a restore workgroup 64;
-// index arithmetic in 32 bits, tensor and head scalar), and issues all of a
-// lane's loads before it uses the first.
+// workgroup takes 96 consecutive (token, tensor, head) rows in the order of
+// the qkv projection, so its reads are one contiguous stretch and its 128-byte
+// rows scatter on the write side (a restore workgroup takes 64 tokens of one
+// head); index arithmetic is in 32 bits and a lane issues all of its loads
+// before it uses the first.
 // Precedent in the reference: kernels/qkv_layout.py:8-157 (layout only).
 #include "common.h"
 
@@ -32,10 +34,10 @@ namespace {
 constexpr int kHeadDim = 64;
 constexpr int kThreads = 256;
 constexpr int kRows = kThreads / 8;  // token rows per pass: 8 lanes per 64-feature row
-// token rows per lane group: the pack kernel's per-row norm and rotary work
-// hides behind four rows' loads; the copy-only restore does best with two
-constexpr int kPackPasses = 4;
-constexpr int kPackTokens = kRows * kPackPasses;
+// rows per lane group: three for the pack kernel (64 VGPRs or fewer, eight
+// waves per SIMD), two for the copy-only restore
+constexpr int kPackPasses = 3;
+constexpr int kPackRows = kRows * kPackPasses;
 constexpr int kPasses = 2;
 constexpr int kTokens = kRows * kPasses;
 
@@ -54,61 +56,61 @@ struct PackParams {
 };
 
 
-// Workgroup (x, b): tensor/head th = x % 3H (0..H-1 q, H..2H-1 k, 2H..3H-1
-// v), tokens [128 (x / 3H), +128) of batch entry b; consecutive workgroups
-// take the heads of the same tokens. Lane group g (8 lanes, 8 features
-// each) handles tokens g, g + 32, g + 64 and g + 96 of the block. Every load
-// (features, positions, then the rotary table entries) is issued before the
-// first result is computed.
+// Workgroup (x, b): rows [kPackRows x, +kPackRows) of batch entry b, where
+// row r is (token r / 3H, tensor/head r % 3H: 0..H-1 q, H..2H-1 k,
+// 2H..3H-1 v). For the usual [B, T, 3, H, 64] qkv projection a workgroup
+// therefore reads one contiguous stretch of it; the 128-byte rows are
+// scattered on the write side. Lane group g (8 lanes, 8 features each)
+// handles rows g, g + 32 and g + 64 of the range. With H a multiple of 8 the
+// eight rows of a wave share their token and tensor. The LayerNorm weights
+// are staged in LDS once per workgroup; the rotary table entries of a row
+// are loaded when the row is computed.
 __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) {
-  const int32_t H = p.H, T = p.N * p.P;
-  const int32_t th = static_cast<int32_t>(blockIdx.x % (3 * H));
-  const int32_t tb = static_cast<int32_t>(blockIdx.x / (3 * H));
-  const int32_t part = th / H, h = th - part * H;
+  const int32_t H = p.H, T = p.N * p.P, R3 = 3 * H;
+  const int32_t rows = T * R3;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x, sub = tid & 7;
-  const bool norm = part < 2 && p.norm[part];
-  const bool rope = part < 2 && p.pos;
-  const uint16_t *src = p.src[part] + b * p.sb[part] + h * p.sh[part] + sub * 8;
-  int32_t t[kPackPasses];
+  // LayerNorm weight and bias of q (0) and k (1), 1 and 0 where absent
+  static_assert(kThreads == 2 * 2 * kHeadDim, "one thread per staged LayerNorm weight or bias");
+  __shared__ floatx4 nrm[2][2][kHeadDim / 4];
+  const bool any_norm = p.norm[0] || p.norm[1];
+  if (any_norm) {
+    const int which = tid >> 7, wb = (tid >> 6) & 1, f = tid & 63;
+    const float *src = wb == 0 ? p.norm_w[which] : p.norm_b[which];
+    reinterpret_cast<float *>(nrm[which][wb])[f] = src ? src[f] : (wb == 0 ? 1.f : 0.f);
+  }
+  int32_t r = static_cast<int32_t>(blockIdx.x) * kPackRows + (tid >> 3);
+  int32_t t = r / R3, th = r - t * R3;
   bool ok[kPackPasses];
+  int32_t tk[kPackPasses], pt[kPackPasses], hd[kPackPasses];
   u32x4 raw[kPackPasses];
   int32_t pq[kPackPasses];
 #pragma unroll
   for (int i = 0; i < kPackPasses; ++i) {
-    t[i] = tb * kPackTokens + i * kRows + (tid >> 3);
-    ok[i] = t[i] < T;
-    const int32_t tc = ok[i] ? t[i] : T - 1;  // in-bounds stand-in for rows past the end
-    raw[i] = *reinterpret_cast<const u32x4 *>(src + static_cast<int64_t>(tc) * p.st[part]);
-    pq[i] = rope ? p.pos[b * p.pos_sb + static_cast<int64_t>(tc) * p.pos_st + (sub >> 2)] : 0;
-  }
-  float cs[kPackPasses][8], sn[kPackPasses][8];
-  if (rope) {
-#pragma unroll
-    for (int i = 0; i < kPackPasses; ++i) {
-      const int32_t q = pq[i] < 0 ? 0 : (pq[i] >= p.rope_n ? p.rope_n - 1 : pq[i]);
-      const floatx4 *c4 = reinterpret_cast<const floatx4 *>(p.rope_cos + q * 16 + (sub & 1) * 8);
-      const floatx4 *s4 = reinterpret_cast<const floatx4 *>(p.rope_sin + q * 16 + (sub & 1) * 8);
-      const floatx4 c0 = c4[0], c1 = c4[1], s0 = s4[0], s1 = s4[1];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        cs[i][e] = c0[e]; cs[i][e + 4] = c1[e];
-        sn[i][e] = s0[e]; sn[i][e + 4] = s1[e];
-      }
-    }
-  }
-  float w[8], bb[8];
-  if (norm) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      w[e] = p.norm_w[part] ? p.norm_w[part][sub * 8 + e] : 1.f;
-      bb[e] = p.norm_b[part] ? p.norm_b[part][sub * 8 + e] : 0.f;
+    ok[i] = r < rows;
+    const int32_t tc = ok[i] ? t : T - 1, thc = ok[i] ? th : 0;  // in-bounds stand-in for rows past the end
+    const int32_t part = (thc >= H) + (thc >= 2 * H);
+    tk[i] = tc; pt[i] = part; hd[i] = thc - part * H;
+    const uint16_t *base = part == 0 ? p.src[0] : (part == 1 ? p.src[1] : p.src[2]);
+    const int64_t sb = part == 0 ? p.sb[0] : (part == 1 ? p.sb[1] : p.sb[2]);
+    const int64_t st = part == 0 ? p.st[0] : (part == 1 ? p.st[1] : p.st[2]);
+    const int64_t sh = part == 0 ? p.sh[0] : (part == 1 ? p.sh[1] : p.sh[2]);
+    raw[i] = *reinterpret_cast<const u32x4 *>(base + b * sb + tc * st + hd[i] * sh + sub * 8);
+    pq[i] = p.pos ? p.pos[b * p.pos_sb + static_cast<int64_t>(tc) * p.pos_st + (sub >> 2)] : 0;
+    r += kRows;
+    th += kRows;
+    while (th >= R3) {
+      th -= R3;
+      ++t;
     }
   }
   const int32_t np = p.N * (p.P - p.S), ns = p.N * p.S;
-  const int64_t bh = b * H + h;
+  if (any_norm) __syncthreads();
 #pragma unroll
   for (int i = 0; i < kPackPasses; ++i) {
+    const int part = pt[i];
+    const bool norm = part < 2 && p.norm[part == 0 ? 0 : 1];
+    const bool rope = part < 2 && p.pos;
     float x[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -116,6 +118,10 @@ __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) 
       x[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(raw[i][e] >> 16));
     }
     if (norm) {
+      const int pn = part == 0 ? 0 : 1;
+      const floatx4 w0 = nrm[pn][0][2 * sub], w1 = nrm[pn][0][2 * sub + 1];
+      const floatx4 b0 = nrm[pn][1][2 * sub], b1 = nrm[pn][1][2 * sub + 1];
+      const float eps = part == 0 ? p.eps[0] : p.eps[1];
       float s = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) s += x[e];
@@ -124,28 +130,37 @@ __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) 
 #pragma unroll
       for (int e = 0; e < 8; ++e) v += (x[e] - mean) * (x[e] - mean);
       const float var = group8_sum(v) / static_cast<float>(kHeadDim);
-      const float rstd = 1.0f / sqrtf(var + p.eps[part]);
+      const float rstd = 1.0f / sqrtf(var + eps);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = ((x[e] - mean) * rstd) * w[e] + bb[e];
+      for (int e = 0; e < 8; ++e) {
+        const float we = e < 4 ? w0[e] : w1[e - 4], be = e < 4 ? b0[e] : b1[e - 4];
+        x[e] = ((x[e] - mean) * rstd) * we + be;
+      }
     }
     if (rope) {
       // features [0, 32) rotate with the row position, [32, 64) with the
       // column position; inside a half, feature j < 16 pairs with j + 16
+      const int32_t q = pq[i] < 0 ? 0 : (pq[i] >= p.rope_n ? p.rope_n - 1 : pq[i]);
+      const floatx4 *c4 = reinterpret_cast<const floatx4 *>(p.rope_cos + q * 16 + (sub & 1) * 8);
+      const floatx4 *s4 = reinterpret_cast<const floatx4 *>(p.rope_sin + q * 16 + (sub & 1) * 8);
+      const floatx4 c0 = c4[0], c1 = c4[1], s0 = s4[0], s1 = s4[1];
       const bool first = (sub & 2) == 0;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float partner = dpp<kQuadXor2>(x[e]);
         const float rot = first ? -partner : partner;
-        x[e] = x[e] * cs[i][e] + rot * sn[i][e];
+        const float ce = e < 4 ? c0[e] : c1[e - 4], se = e < 4 ? s0[e] : s1[e - 4];
+        x[e] = x[e] * ce + rot * se;
       }
     }
     if (!ok[i]) continue;
     u32x4 out;
 #pragma unroll
     for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(x[2 * e], x[2 * e + 1]);
-    const int32_t n = t[i] / p.P, tf = t[i] - n * p.P;
+    const int32_t n = tk[i] / p.P, tf = tk[i] - n * p.P;
     const bool patch = tf >= p.S;
     const int32_t ip = n * (p.P - p.S) + (tf - p.S), is = n * p.S + tf;
+    const int64_t bh = b * H + hd[i];
     uint16_t *dst;
     if (part == 0)
       dst = patch ? p.q_patch + (bh * np + ip) * kHeadDim : p.q_special + (bh * ns + is) * kHeadDim;
@@ -214,7 +229,7 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   VASC_REQUIRE(B > 0 && H > 0 && N > 0 && P > 0 && S >= 0 && S <= P, "invalid sizes B=%lld H=%lld N=%lld P=%lld S=%lld",
                (long long)B, (long long)H, (long long)N, (long long)P, (long long)S);
   VASC_REQUIRE(B < 65536 && H < 4096 && N * P < (int64_t(1) << 31) / 64, "too many tokens or heads");
-  VASC_REQUIRE(cdiv(N * P, kPackTokens) * 3 * H < (int64_t(1) << 31), "grid too large");
+  VASC_REQUIRE(N * P * 3 * H < (int64_t(1) << 31) - 4 * kPackRows, "too many (token, head) rows");
   int rc;
   if ((rc = check_src("q", q, q_sb, q_st, q_sh))) return rc;
   if ((rc = check_src("k", k, k_sb, k_st, k_sh))) return rc;
@@ -246,7 +261,7 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   p.rope_cos = rope_cos; p.rope_sin = rope_sin;
   p.rope_n = static_cast<int32_t>(rope_n < (int64_t(1) << 30) ? rope_n : (int64_t(1) << 30));
   p.q_patch = q_patch; p.q_special = q_special; p.k_out = k_out; p.v_out = v_out;
-  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(cdiv(N * P, kPackTokens) * 3 * H), static_cast<unsigned>(B)),
+  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(cdiv(N * P * 3 * H, kPackRows)), static_cast<unsigned>(B)),
                      dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
   return check_launch("vasc_pack_qkv");
 }
