@@ -41,7 +41,7 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 
 
-TRAFFIC_SUMMARY = "profiles/traffic_c2_step.md"
+TRAFFIC_SUMMARY = "profiles/traffic_c2_forward.md"
 
 
 def traffic_bytes():
@@ -149,6 +149,19 @@ def attention_min_bytes(index, count, n_q, n_k, d):
     blocks = int(touched[..., :kb].sum().item())
     heads = index.shape[0] * index.shape[1]
     return heads * n_q * d * 2 * 2 + blocks * 64 * d * 2 * 2, blocks / heads
+
+
+def attention_min_bytes_global(index, count, n_patch, n_total, n_special, H, d):
+    """Least HBM bytes of one global-layer attention launch (B = 1): the patch
+    and special queries read and their outputs written once, and every K
+    block and packed V tile read once; the special queries attend to every
+    key block, so each one is needed. Also returns the distinct key blocks
+    the patch queries' lists name per head."""
+    patch_only, listed = attention_min_bytes(index, count, n_patch, n_total, d)
+    if n_special == 0:
+        return patch_only, listed
+    kb = -(-n_total // 64)
+    return H * (n_patch + n_special) * d * 2 * 2 + H * kb * 64 * d * 2 * 2, listed
 
 
 def hbm_bytes_per_launch(H, n_patch, n_total, d, listed_per_layer):
@@ -839,12 +852,25 @@ def main() -> int:
         log("aggregator probe done")
         return 0
     if args.probe == "traffic":
-        layers = [synthetic_layer(frames, 1041, 5, 16, 64, seed=li, device=dev) for li in range(24)]
+        # a 256 MiB copy (the FETCH_SIZE / WRITE_SIZE scale), then one untimed
+        # vasc forward of the headline aggregator
+        from vasc_amd import install
         src = torch.empty(128 * 2**20, dtype=torch.bfloat16, device=dev).normal_()
         dst = torch.empty_like(src)
-        dst.copy_(src)  # 256 MiB read + 256 MiB written: the FETCH_SIZE / WRITE_SIZE scale
-        run_step(layers, ratios, pipeline.Ledger(), Timer(enabled=False))
+        dst.copy_(src)
+        del src, dst
+        agg = build_aggregator(dev)
+        g = torch.Generator(device=dev).manual_seed(0)
+        images = torch.rand(1, frames, 3, 392, 518, device=dev, generator=g)
+        with _ModeEnv("vggt", "vasc"), torch.no_grad(), AttnLaunchEvents(len(agg.global_blocks)) as ev:
+            install.sparse_aggregator_from_vggt_layerwise(agg, layer_sparsity_ratios=ratios, verbose=False)
+            ev.enabled = True
+            agg(images)
+            ev.enabled = False
         torch.cuda.synchronize()
+        mins = [attention_min_bytes_global(*lst) for lst in ev.lists.values()]
+        log(f"attention_min_bytes_per_launch: {statistics.fmean(m for m, _ in mins):.0f}")
+        log(f"distinct_key_blocks_per_head_patch_queries: {statistics.fmean(b for _, b in mins):.2f}")
         log("traffic probe done")
         return 0
 

@@ -110,9 +110,10 @@ def test_global_attn_patch_and_special_in_one_launch():
     rng = np.random.default_rng(25)
     idx = np.full((B, H, qb, nkb), -1, np.int32)
     cnt = rng.integers(1, nkb + 1, size=(B, H, qb)).astype(np.int32)
-    for h in range(H):
-        for i in range(qb):
-            idx[0, h, i, : cnt[0, h, i]] = np.sort(rng.choice(nkb, cnt[0, h, i], replace=False))
+    for bb in range(B):
+        for h in range(H):
+            for i in range(qb):
+                idx[bb, h, i, : cnt[bb, h, i]] = np.sort(rng.choice(nkb, cnt[bb, h, i], replace=False))
     index, count = torch.from_numpy(idx).cuda(), torch.from_numpy(cnt).cuda()
     vt = ops.pack_v(v)
     o_p, o_s = ops.global_attn(q, qs, k, vt, index, count)
@@ -127,13 +128,14 @@ def test_global_attn_patch_and_special_in_one_launch():
     assert none is None and np.array_equal(_bits(o_p2), _bits(o_p))
 
 
-@pytest.mark.parametrize("N,P,S,H", [(3, 1041, 5, 2), (4, 70, 0, 1), (2, 7, 7 - 1, 2)])
-def test_global_attn_tokens_equals_attention_then_restore(N, P, S, H):
+@pytest.mark.parametrize("N,P,S,H,B", [(3, 1041, 5, 2, 1), (4, 70, 0, 1, 1), (2, 7, 7 - 1, 2, 1), (2, 37, 4, 2, 2)])
+def test_global_attn_tokens_equals_attention_then_restore(N, P, S, H, B):
     """vasc_global_attn_tokens_fwd writes every result on its frame-major
     token row: bit-identical to vasc_global_attn_fwd followed by the restore
-    kernel (frames with and without special tokens, a ragged last block)."""
+    kernel (frames with and without special tokens, a ragged last block, a
+    batch of two)."""
     from vasc_amd import ops
-    B, D = 1, 64
+    D = 64
     Np, Ns, Tk = N * (P - S), N * S, N * P
     q = _bf16((B, H, Np, D), 31).cuda()
     qs = _bf16((B, H, Ns, D), 32).cuda() if S else None
@@ -143,9 +145,10 @@ def test_global_attn_tokens_equals_attention_then_restore(N, P, S, H):
     rng = np.random.default_rng(35)
     idx = np.full((B, H, qb, nkb), -1, np.int32)
     cnt = rng.integers(1, nkb + 1, size=(B, H, qb)).astype(np.int32)
-    for h in range(H):
-        for i in range(qb):
-            idx[0, h, i, : cnt[0, h, i]] = np.sort(rng.choice(nkb, cnt[0, h, i], replace=False))
+    for bb in range(B):
+        for h in range(H):
+            for i in range(qb):
+                idx[bb, h, i, : cnt[bb, h, i]] = np.sort(rng.choice(nkb, cnt[bb, h, i], replace=False))
     index, count = torch.from_numpy(idx).cuda(), torch.from_numpy(cnt).cuda()
     vt = ops.pack_v(v)
     o_p, o_s = ops.global_attn(q, qs, k, vt, index, count)

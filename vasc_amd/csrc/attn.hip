@@ -42,9 +42,11 @@
 //    query blocks of the same head (K/V reuse in that XCD's L2).
 //  * vasc_global_attn_fwd adds the layer's special-token queries, which
 //    attend to every key (attention.py:8480-8484), to the same launch: their
-//    workgroups take the first hardware ids, so they spread over all XCDs
-//    and start first (each walks every key block, about four times the
-//    work of a patch-query workgroup).
+//    workgroups take the first hardware ids, so they start first (each walks
+//    every key block, about four times the work of a patch-query
+//    workgroup), and they are remapped like the patch workgroups, so each
+//    XCD takes the special queries of the heads whose patch queries it
+//    walks and reads their K and V through the same L2.
 #include "common.h"
 
 namespace vasc {
@@ -76,7 +78,7 @@ struct AttnParams {
   int64_t q2_sb, q2_sh, q2_st;
   uint16_t *o2;
   int64_t o2_sb, o2_sh, o2_st;
-  int64_t nq2, nq2b, num_wg2;
+  int64_t nq2, nq2b, num_wg2, num_wg2_slots;
   // token-major output (tok_p > 0): query rows land on the frame-major token
   // rows of o (frames of tok_p tokens, tok_s special ones first)
   int64_t tok_p, tok_s;
@@ -125,12 +127,14 @@ void bsattn_fwd_kernel(const AttnParams p) {
   __shared__ float pv_gap[kPv ? 4 : 1];                                 // per-wave gap of the PV post-cut
   auto lds_u32 = [](const uint16_t *ptr) { return lds_addr32(ptr); };
 
-  // Workgroups [0, num_wg2) take the special-token queries (every key
-  // block); the rest the patch queries of their lists.
-  const bool dense = kDense || static_cast<int64_t>(blockIdx.x) < p.num_wg2;
+  // Workgroups [0, num_wg2_slots) take the special-token queries (every key
+  // block; the slot count is rounded up to a multiple of the 8 XCDs so that
+  // both ranges start on XCD 0); the rest the patch queries of their lists.
+  const bool dense = kDense || static_cast<int64_t>(blockIdx.x) < p.num_wg2_slots;
   const int64_t nqb = dense && !kDense ? p.nq2b : p.nqb;
-  const int64_t wg = dense && !kDense ? static_cast<int64_t>(blockIdx.x)
-                                      : xcd_remap(static_cast<int64_t>(blockIdx.x) - p.num_wg2, p.num_wg);
+  const int64_t wg = dense && !kDense ? xcd_remap(static_cast<int64_t>(blockIdx.x), p.num_wg2_slots)
+                                      : xcd_remap(static_cast<int64_t>(blockIdx.x) - p.num_wg2_slots, p.num_wg);
+  if (dense && !kDense && wg >= p.num_wg2) return;  // padding of the special-query slots
   const int qb = static_cast<int>(wg % nqb);
   const int64_t bh = wg / nqb;
   const int64_t h = bh % p.H;
@@ -494,7 +498,8 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
   p.nq2 = sq.q2 ? sq.nq2 : 0;
   p.nq2b = cdiv(p.nq2, kBlockQ);
   p.num_wg2 = B * H * p.nq2b;
-  VASC_REQUIRE(p.num_wg + p.num_wg2 < (int64_t(1) << 31), "grid too large");
+  p.num_wg2_slots = (p.num_wg2 + 7) / 8 * 8;
+  VASC_REQUIRE(p.num_wg + p.num_wg2_slots < (int64_t(1) << 31), "grid too large");
   VASC_SUPPORTED(nk < (int64_t(1) << 30) && nq < (int64_t(1) << 40), "sequence of %lld keys not built (< 2^30)",
                  (long long)nk);
   p.pv_thr = pv_thr;
@@ -504,7 +509,7 @@ int launch_attn(bool dense, const uint16_t *q, int64_t q_sb, int64_t q_sh, int64
   p.tok_s = ot.S;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   auto kern = dense ? bsattn_fwd_kernel<true> : (pv_thr ? bsattn_fwd_kernel<false, true> : bsattn_fwd_kernel<false>);
-  hipLaunchKernelGGL(kern, dim3(p.num_wg + p.num_wg2), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL(kern, dim3(p.num_wg + p.num_wg2_slots), dim3(kThreads), 0, s, p);
   return check_launch(dense ? "vasc_dense_attn_fwd" : "vasc_block_sparse_attn_fwd");
 }
 
