@@ -59,7 +59,11 @@ def test_pack_from_head_major_views():
     assert np.array_equal(_to_np(vo), OL.reorder_to_patch_then_special(v.float().numpy(), N, P, S))
 
 
-def test_pack_norm_and_rotary():
+@pytest.mark.parametrize("which", ["both", "q_only", "k_only"])
+def test_pack_norm_and_rotary(which):
+    """Per-head LayerNorm of q and/or k, then the 2D rotary embedding, against
+    the oracle (the LayerNorm weights are staged per workgroup, so the
+    one-sided cases check that the other tensor's rows stay untouched)."""
     from vasc_amd import ops
     from vasc_amd.aggregator import RotaryPositionEmbedding2D
     N, Hp, Wp, S, H, D = 3, 9, 13, 5, 2, 64
@@ -72,10 +76,14 @@ def test_pack_norm_and_rotary():
     pos = frame_pos.repeat(N, 1)  # [T, 2]
     cos, sin = RotaryPositionEmbedding2D().tables(D, "cuda")
     x = qkv.cuda().view(1, N * P, 3, H, D)
-    qp, qs, k, v = ops.pack_qkv(x[:, :, 0], x[:, :, 1], x[:, :, 2], N, P, S, q_norm=(qw.cuda(), qb.cuda(), 1e-6),
-                                k_norm=(kw.cuda(), None, 1e-5), pos=pos.cuda(), rope_tables=(cos, sin))
-    rp, rs, rk, rv = OL.pack_layer(qkv.float().numpy(), N, P, S, H, q_norm=(qw.numpy(), qb.numpy(), 1e-6),
-                                   k_norm=(kw.numpy(), None, 1e-5), pos=pos.numpy(),
+    use_q, use_k = which in ("both", "q_only"), which in ("both", "k_only")
+    qp, qs, k, v = ops.pack_qkv(x[:, :, 0], x[:, :, 1], x[:, :, 2], N, P, S,
+                                q_norm=(qw.cuda(), qb.cuda(), 1e-6) if use_q else None,
+                                k_norm=(kw.cuda(), None, 1e-5) if use_k else None, pos=pos.cuda(),
+                                rope_tables=(cos, sin))
+    rp, rs, rk, rv = OL.pack_layer(qkv.float().numpy(), N, P, S, H,
+                                   q_norm=(qw.numpy(), qb.numpy(), 1e-6) if use_q else None,
+                                   k_norm=(kw.numpy(), None, 1e-5) if use_k else None, pos=pos.numpy(),
                                    tables=(cos.cpu().numpy(), sin.cpu().numpy()))
     for got, ref in ((qp, rp), (qs, rs), (k, rk)):
         err = np.abs(_to_np(got) - ref)

@@ -76,7 +76,8 @@ __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) 
   const bool any_norm = p.norm[0] || p.norm[1];
   if (any_norm) {
     const int which = tid >> 7, wb = (tid >> 6) & 1, f = tid & 63;
-    const float *src = wb == 0 ? p.norm_w[which] : p.norm_b[which];
+    // a tensor without the norm may pass any pointer: read only the normed one's
+    const float *src = !p.norm[which] ? nullptr : (wb == 0 ? p.norm_w[which] : p.norm_b[which]);
     reinterpret_cast<float *>(nrm[which][wb])[f] = src ? src[f] : (wb == 0 ? 1.f : 0.f);
   }
   int32_t r = static_cast<int32_t>(blockIdx.x) * kPackRows + (tid >> 3);

@@ -365,6 +365,8 @@ def global_attn_tokens(q_patch: torch.Tensor, q_special: torch.Tensor | None, k:
     nk = k.shape[2]
     if n_patch != N * (P - S) or nk != N * P:
         raise ValueError(f"q_patch/k hold {n_patch}/{nk} tokens, expected {N * (P - S)}/{N * P}")
+    if k.shape[:2] != (B, H) or k.shape[3] != D:
+        raise ValueError(f"k {tuple(k.shape)} does not match q_patch {tuple(q_patch.shape)}")
     if vt.shape != (B, H, math.ceil(nk / BLOCK_K), D, BLOCK_K):
         raise ValueError(f"vt shape {tuple(vt.shape)} does not match K {tuple(k.shape)}")
     qb = math.ceil(n_patch / BLOCK_Q)
@@ -374,8 +376,8 @@ def global_attn_tokens(q_patch: torch.Tensor, q_special: torch.Tensor | None, k:
         raise ValueError(f"index/count must be [B,H,{qb},W]/[B,H,{qb}]")
     qs_args = (None, 0, 0, 8)
     if S > 0:
-        if q_special is None or q_special.shape[2] != N * S:
-            raise ValueError(f"q_special must hold {N * S} tokens")
+        if q_special is None or tuple(q_special.shape) != (B, H, N * S, D):
+            raise ValueError(f"q_special must be [B, H, {N * S}, {D}]")
         q_special = _bhtd(q_special, "q_special")
         qs_args = (q_special.data_ptr(), *q_special.stride()[:3])
     out = torch.empty(B, N * P, H * D, device=q_patch.device, dtype=torch.bfloat16)
