@@ -335,6 +335,46 @@ def test_pv_post_cut_service_through_block_sparse_attn(release_env, monkeypatch)
     assert SW.finalize_cosa_value_risk_pair_debt(st)
 
 
+def test_global_layer_pv_path_matches_release_path():
+    """A finite PV threshold that never cuts (1e9 log2 units) sends the layer
+    through the PV post-cut attention instance, the separate special-query
+    launch and the restore kernel; the release threshold (1e10, inert) through
+    the one token-major launch. Both give the same layer output, bit for bit."""
+    from vasc_amd.attention import adaptive_sparse_attention_forward
+
+    class Attn(torch.nn.Module):
+        def __init__(self, dim, heads):
+            super().__init__()
+            self.qkv = torch.nn.Linear(dim, 3 * dim)
+            self.proj = torch.nn.Linear(dim, dim)
+            self.q_norm = torch.nn.LayerNorm(dim // heads)
+            self.k_norm = torch.nn.LayerNorm(dim // heads)
+            self.rope = None
+            self.heads = heads
+
+    torch.manual_seed(6)
+    N, Hp, Wp, S, heads, dim = 3, 10, 13, 5, 4, 256
+    P = Hp * Wp + S
+    m = Attn(dim, heads).cuda().to(torch.bfloat16)
+    x = torch.randn(1, N * P, dim, device="cuda", dtype=torch.bfloat16)
+    ys, xs = torch.meshgrid(torch.arange(Hp), torch.arange(Wp), indexing="ij")
+    patch_pos = torch.stack([ys.reshape(-1), xs.reshape(-1)], -1) + 1
+    pos = torch.cat([torch.zeros(S, 2, dtype=torch.long), patch_pos]).expand(N, P, 2).cuda()
+    saved = {k: os.environ.pop(k) for k in list(os.environ) if k.startswith("SPARSE_VGGT_")}
+    outs = []
+    try:
+        for thr in ("1e10", "1e9"):
+            os.environ["SPARSE_VGGT_OFFICIAL_MASK"] = "1"
+            os.environ["SPARSE_VGGT_QK_PV_THRESHOLD"] = thr
+            outs.append(adaptive_sparse_attention_forward(m, x, pos, sparse_ratio=0.5, num_special_tokens=S,
+                                                          num_heads=heads, routing_state={}))
+    finally:
+        for k in ("SPARSE_VGGT_OFFICIAL_MASK", "SPARSE_VGGT_QK_PV_THRESHOLD"):
+            os.environ.pop(k, None)
+        os.environ.update(saved)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 def test_global_layer_forward_dense_limit():
     """adaptive_sparse_attention_forward at sparsity 0 equals dense attention of
     the same module (all key blocks kept)."""
