@@ -386,6 +386,9 @@ int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
  * Outputs (contiguous bf16): q_patch [B,H,N*(P-S),d], q_special [B,H,N*S,d],
  *   k_out / v_out [B,H,T,d] with the patch tokens of all frames first, then
  *   the special tokens. Arithmetic in float32, one bf16 rounding per output.
+ *   v_out == NULL: v is not packed (v may then be NULL); a caller that packs
+ *   V for attention straight from the projection (vasc_pack_v takes strided
+ *   rows) skips writing and re-reading it.
  * Built variant: d == 64.
  */
 int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int64_t q_sh,

@@ -91,6 +91,28 @@ def test_pack_norm_and_rotary(which):
     assert np.array_equal(_to_np(v), rv)
 
 
+@pytest.mark.parametrize("N,P,S,H", [(1, 1041, 0, 16), (3, 70, 5, 3)])
+def test_pack_without_v_and_strided_v_tiles(N, P, S, H):
+    """pack_qkv with v=None writes the same q and k as the full pack (the row
+    space then spans q and k only), and V tiles packed straight from the
+    projection's strided rows equal those packed from the packed v (frame
+    layers: S = 0, the order unchanged)."""
+    from vasc_amd import ops
+    D = 64
+    qkv = _bf16((2, N * P, 3 * H * D), N * 7 + P).cuda().view(2, N * P, 3, H, D)
+    w = torch.randn(D, generator=torch.Generator().manual_seed(3)).cuda()
+    full = ops.pack_qkv(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], N, P, S, q_norm=(w, None, 1e-6))
+    part = ops.pack_qkv(qkv[:, :, 0], qkv[:, :, 1], None, N, P, S, q_norm=(w, None, 1e-6))
+    assert part[3] is None
+    for a, b in zip(full[:3], part[:3]):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert np.array_equal(_bits(a), _bits(b))
+    if S == 0:
+        vt_strided = ops.pack_v(qkv[:, :, 2].transpose(1, 2))
+        assert np.array_equal(_bits(vt_strided), _bits(ops.pack_v(full[3])))
+
+
 @pytest.mark.parametrize("N,P,S", [(3, 1041, 5), (2, 50, 0), (2, 7, 7)])
 def test_restore_bit_exact(N, P, S):
     from vasc_amd import ops

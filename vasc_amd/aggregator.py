@@ -98,13 +98,16 @@ class Attention(nn.Module):
         B, T, dim = x.shape
         H, D = self.num_heads, self.head_dim
         qkv = self.qkv(x).to(torch.bfloat16).view(B, T, 3, H, D)
-        qp, _, k, v = ops.pack_qkv(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], 1, T, 0,
+        qp, _, k, _ = ops.pack_qkv(qkv[:, :, 0], qkv[:, :, 1], None, 1, T, 0,
                                    q_norm=layer_norm_args(self.q_norm), k_norm=layer_norm_args(self.k_norm),
                                    pos=pos if self.rope is not None else None,
                                    rope_tables=self._tables(pos, D, x.device))
+        # V needs neither norm nor rotation: its MFMA tiles are packed straight
+        # from the projection's strided rows
+        vt = ops.pack_v(qkv[:, :, 2].transpose(1, 2))
         # the kernel writes straight into the frame-major [B, T, H*D] rows proj reads
         out = torch.empty(B, T, H * D, device=x.device, dtype=torch.bfloat16)
-        ops.dense_attn(qp, k, ops.pack_v(v), scale=1.0 / math.sqrt(D), out=out.view(B, T, H, D).transpose(1, 2))
+        ops.dense_attn(qp, k, vt, scale=1.0 / math.sqrt(D), out=out.view(B, T, H, D).transpose(1, 2))
         return self.proj_drop(self.proj(out.to(x.dtype)))
 
     def _tables(self, pos, head_dim, device):

@@ -66,7 +66,8 @@ struct PackParams {
 // are staged in LDS once per workgroup; the rotary table entries of a row
 // are loaded when the row is computed.
 __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) {
-  const int32_t H = p.H, T = p.N * p.P, R3 = 3 * H;
+  // rows per token: q and k of every head, and v unless it is not packed
+  const int32_t H = p.H, T = p.N * p.P, R3 = (p.v_out ? 3 : 2) * H;
   const int32_t rows = T * R3;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x, sub = tid & 7;
@@ -234,8 +235,8 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   int rc;
   if ((rc = check_src("q", q, q_sb, q_st, q_sh))) return rc;
   if ((rc = check_src("k", k, k_sb, k_st, k_sh))) return rc;
-  if ((rc = check_src("v", v, v_sb, v_st, v_sh))) return rc;
-  VASC_REQUIRE(k_out && v_out, "k_out and v_out are required");
+  if (v_out && (rc = check_src("v", v, v_sb, v_st, v_sh))) return rc;
+  VASC_REQUIRE(k_out, "k_out is required");
   VASC_REQUIRE(P == S || q_patch, "q_patch is required when frames hold patch tokens");
   VASC_REQUIRE(S == 0 || q_special, "q_special is required when frames hold special tokens");
   for (const void *o : {static_cast<const void *>(q_patch), static_cast<const void *>(q_special),

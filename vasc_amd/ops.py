@@ -460,11 +460,12 @@ def residual_norm(x: torch.Tensor, y: torch.Tensor, gamma: torch.Tensor | None =
     return xo, no
 
 
-def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, frames: int, tokens_per_frame: int,
+def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, frames: int, tokens_per_frame: int,
              special: int, *, q_norm=None, k_norm=None, pos: torch.Tensor | None = None,
              rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None):
     """Frame-major ``[B,T,H,D]`` q/k/v views -> ``(q_patch, q_special, k, v)``
     in the global layer's ``[patch; special]`` order, ``[B,H,*,D]`` bf16.
+    ``v=None`` packs only q and k (the returned v is None).
 
     ``q_norm`` / ``k_norm``: ``(weight or None, bias or None, eps)`` of a
     per-head LayerNorm, or None. ``pos`` int ``[B,T,2]`` (row, column) with
@@ -472,13 +473,14 @@ def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, frames: int, tok
     """
     B, T, H, D = q.shape
     N, P, S = int(frames), int(tokens_per_frame), int(special)
-    if N * P != T or k.shape != q.shape or v.shape != q.shape:
-        raise ValueError(f"q/k/v must be [B,{N}*{P},H,D], got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if N * P != T or k.shape != q.shape or (v is not None and v.shape != q.shape):
+        raise ValueError(f"q/k/v must be [B,{N}*{P},H,D], got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{None if v is None else tuple(v.shape)}")
     dev = q.device
     qp = torch.empty(B, H, N * (P - S), D, device=dev, dtype=torch.bfloat16)
     qs = torch.empty(B, H, N * S, D, device=dev, dtype=torch.bfloat16)
     ko = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
-    vo = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+    vo = None if v is None else torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
     keep = []
 
     def norm_args(nrm, name):
@@ -517,9 +519,10 @@ def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, frames: int, tok
         rope = (pos32.data_ptr(), pos32.stride(0) if pos32.shape[0] > 1 else 0, pos32.stride(1), cos.data_ptr(),
                 sin.data_ptr(), cos.shape[0])
     qn, kn = norm_args(q_norm, "q_norm"), norm_args(k_norm, "k_norm")
-    _lib.call("vasc_pack_qkv", *_btht(q, "q"), *_btht(k, "k"), *_btht(v, "v"), B, H, N, P, S, D,
+    vsrc = (None, 0, 0, 0) if v is None else _btht(v, "v")
+    _lib.call("vasc_pack_qkv", *_btht(q, "q"), *_btht(k, "k"), *vsrc, B, H, N, P, S, D,
               qn[0], qn[1], qn[2], qn[3], kn[0], kn[1], kn[2], kn[3], *rope,
-              qp.data_ptr(), qs.data_ptr(), ko.data_ptr(), vo.data_ptr(), _stream())
+              qp.data_ptr(), qs.data_ptr(), ko.data_ptr(), _ptr(vo), _stream())
     return qp, (qs if S else None), ko, vo
 
 
