@@ -20,10 +20,11 @@
 // so a row is one 128-byte segment on both sides; the LayerNorm sums are
 // xor butterflies inside the 8-lane group and the rotary partner of a
 // feature (16 places away inside its half) sits two lanes away. A pack
-// workgroup takes 96 consecutive (token, tensor, head) rows in the order of
-// the qkv projection, so its reads are one contiguous stretch and its 128-byte
-// rows scatter on the write side (a restore workgroup takes 64 tokens of one
-// head); index arithmetic is in 32 bits and a lane issues all of its loads
+// workgroup takes twelve groups of eight (token, tensor, head) rows in the
+// order of the qkv projection, so its reads are one contiguous stretch and
+// its 128-byte rows scatter on the write side; a wave's rows share token and
+// tensor, which keeps the index arithmetic on the scalar unit (a restore
+// workgroup takes 64 tokens of one head). A lane issues all of its loads
 // before it uses the first.
 // Precedent in the reference: kernels/qkv_layout.py:8-157 (layout only).
 #include "common.h"
@@ -37,7 +38,7 @@ constexpr int kRows = kThreads / 8;  // token rows per pass: 8 lanes per 64-feat
 // rows per lane group: three for the pack kernel (64 VGPRs or fewer, eight
 // waves per SIMD), two for the copy-only restore
 constexpr int kPackPasses = 3;
-constexpr int kPackRows = kRows * kPackPasses;
+constexpr int kPackGroups = 4 * kPackPasses;  // row groups of eight per pack workgroup
 constexpr int kPasses = 2;
 constexpr int kTokens = kRows * kPasses;
 
@@ -56,21 +57,25 @@ struct PackParams {
 };
 
 
-// Workgroup (x, b): rows [kPackRows x, +kPackRows) of batch entry b, where
-// row r is (token r / 3H, tensor/head r % 3H: 0..H-1 q, H..2H-1 k,
-// 2H..3H-1 v). For the usual [B, T, 3, H, 64] qkv projection a workgroup
-// therefore reads one contiguous stretch of it; the 128-byte rows are
-// scattered on the write side. Lane group g (8 lanes, 8 features each)
-// handles rows g, g + 32 and g + 64 of the range. With H a multiple of 8 the
-// eight rows of a wave share their token and tensor. The LayerNorm weights
-// are staged in LDS once per workgroup; the rotary table entries of a row
-// are loaded when the row is computed.
+// Workgroup (x, b): row groups [12 x, +12) of batch entry b. A row group is
+// eight (token, tensor, head) rows of one token and one tensor: group g is
+// token g / G, tensor (g % G) / H8 (0 q, 1 k, 2 v) and heads 8 ((g % G) % H8)
+// onward, with H8 = ceil(H / 8) groups per tensor and G = 3 H8 (2 H8 when v is
+// not packed). Wave w takes groups 4i + w of the range in passes i = 0..2, so
+// the token and the tensor of every row a wave holds are wave-uniform (the
+// address arithmetic is scalar); lane group j of the wave takes head 8 (..) + j
+// (lanes past H idle). For the usual [B, T, 3, H, 64] qkv projection a
+// workgroup reads one contiguous stretch of it; the 128-byte rows scatter on
+// the write side. The LayerNorm weights are staged in LDS once per
+// workgroup; the rotary table entries of a row are loaded when the row is
+// computed.
 __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) {
-  // rows per token: q and k of every head, and v unless it is not packed
-  const int32_t H = p.H, T = p.N * p.P, R3 = (p.v_out ? 3 : 2) * H;
-  const int32_t rows = T * R3;
+  const int32_t H = p.H, T = p.N * p.P;
+  const int32_t H8 = (H + 7) >> 3, G = (p.v_out ? 3 : 2) * H8;
+  const int32_t groups = T * G;
   const int64_t b = blockIdx.y;
-  const int tid = threadIdx.x, sub = tid & 7;
+  const int tid = threadIdx.x, sub = tid & 7, hl = (tid >> 3) & 7;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // LayerNorm weight and bias of q (0) and k (1), 1 and 0 where absent
   static_assert(kThreads == 2 * 2 * kHeadDim, "one thread per staged LayerNorm weight or bias");
   __shared__ floatx4 nrm[2][2][kHeadDim / 4];
@@ -81,30 +86,28 @@ __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) 
     const float *src = !p.norm[which] ? nullptr : (wb == 0 ? p.norm_w[which] : p.norm_b[which]);
     reinterpret_cast<float *>(nrm[which][wb])[f] = src ? src[f] : (wb == 0 ? 1.f : 0.f);
   }
-  int32_t r = static_cast<int32_t>(blockIdx.x) * kPackRows + (tid >> 3);
-  int32_t t = r / R3, th = r - t * R3;
   bool ok[kPackPasses];
   int32_t tk[kPackPasses], pt[kPackPasses], hd[kPackPasses];
   u32x4 raw[kPackPasses];
   int32_t pq[kPackPasses];
 #pragma unroll
   for (int i = 0; i < kPackPasses; ++i) {
-    ok[i] = r < rows;
-    const int32_t tc = ok[i] ? t : T - 1, thc = ok[i] ? th : 0;  // in-bounds stand-in for rows past the end
-    const int32_t part = (thc >= H) + (thc >= 2 * H);
-    tk[i] = tc; pt[i] = part; hd[i] = thc - part * H;
+    const int32_t grp = static_cast<int32_t>(blockIdx.x) * (4 * kPackPasses) + 4 * i + w;
+    const bool gv = grp < groups;
+    const int32_t g = gv ? grp : groups - 1;  // in-bounds stand-in for groups past the end
+    const int32_t t = __builtin_amdgcn_readfirstlane(g / G);
+    const int32_t rem = g - t * G;
+    const int32_t part = __builtin_amdgcn_readfirstlane(rem / H8);
+    const int32_t h = (rem - part * H8) * 8 + hl;
+    ok[i] = gv && h < H;
+    const int32_t hc = h < H ? h : H - 1;
+    tk[i] = t; pt[i] = part; hd[i] = hc;
     const uint16_t *base = part == 0 ? p.src[0] : (part == 1 ? p.src[1] : p.src[2]);
     const int64_t sb = part == 0 ? p.sb[0] : (part == 1 ? p.sb[1] : p.sb[2]);
     const int64_t st = part == 0 ? p.st[0] : (part == 1 ? p.st[1] : p.st[2]);
     const int64_t sh = part == 0 ? p.sh[0] : (part == 1 ? p.sh[1] : p.sh[2]);
-    raw[i] = *reinterpret_cast<const u32x4 *>(base + b * sb + tc * st + hd[i] * sh + sub * 8);
-    pq[i] = p.pos ? p.pos[b * p.pos_sb + static_cast<int64_t>(tc) * p.pos_st + (sub >> 2)] : 0;
-    r += kRows;
-    th += kRows;
-    while (th >= R3) {
-      th -= R3;
-      ++t;
-    }
+    raw[i] = *reinterpret_cast<const u32x4 *>(base + b * sb + static_cast<int64_t>(t) * st + hc * sh + sub * 8);
+    pq[i] = p.pos ? p.pos[b * p.pos_sb + static_cast<int64_t>(t) * p.pos_st + (sub >> 2)] : 0;
   }
   const int32_t np = p.N * (p.P - p.S), ns = p.N * p.S;
   if (any_norm) __syncthreads();
@@ -231,7 +234,7 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   VASC_REQUIRE(B > 0 && H > 0 && N > 0 && P > 0 && S >= 0 && S <= P, "invalid sizes B=%lld H=%lld N=%lld P=%lld S=%lld",
                (long long)B, (long long)H, (long long)N, (long long)P, (long long)S);
   VASC_REQUIRE(B < 65536 && H < 4096 && N * P < (int64_t(1) << 31) / 64, "too many tokens or heads");
-  VASC_REQUIRE(N * P * 3 * H < (int64_t(1) << 31) - 4 * kPackRows, "too many (token, head) rows");
+  VASC_REQUIRE(N * P * 3 * ((H + 7) / 8) < (int64_t(1) << 31) - kPackGroups, "too many (token, head) rows");
   int rc;
   if ((rc = check_src("q", q, q_sb, q_st, q_sh))) return rc;
   if ((rc = check_src("k", k, k_sb, k_st, k_sh))) return rc;
@@ -263,7 +266,7 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   p.rope_cos = rope_cos; p.rope_sin = rope_sin;
   p.rope_n = static_cast<int32_t>(rope_n < (int64_t(1) << 30) ? rope_n : (int64_t(1) << 30));
   p.q_patch = q_patch; p.q_special = q_special; p.k_out = k_out; p.v_out = v_out;
-  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(cdiv(N * P * 3 * H, kPackRows)), static_cast<unsigned>(B)),
+  hipLaunchKernelGGL(pack_qkv_kernel, dim3(static_cast<unsigned>(cdiv(N * P * (v_out ? 3 : 2) * ((H + 7) / 8), kPackGroups)), static_cast<unsigned>(B)),
                      dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
   return check_launch("vasc_pack_qkv");
 }
