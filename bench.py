@@ -343,21 +343,10 @@ def build_aggregator(dev, seed: int = 0):
     return agg.to(torch.bfloat16).eval()
 
 
-class _ModeEnv:
-    """The reference's SPARSE_VGGT_* switches of one release mode."""
-
-    def __init__(self, backbone, mode):
-        from vasc_amd.launcher import method_environment
-        self.env = method_environment(backbone, mode)
-
-    def __enter__(self):
-        self.saved = {k: os.environ.pop(k) for k in list(os.environ) if k.startswith("SPARSE_VGGT_")}
-        os.environ.update(self.env)
-
-    def __exit__(self, *exc):
-        for k in [k for k in os.environ if k.startswith("SPARSE_VGGT_")]:
-            del os.environ[k]
-        os.environ.update(self.saved)
+def _ModeEnv(backbone: str, mode: str):
+    """The reference's SPARSE_VGGT_* switches of one release mode for a block."""
+    from vasc_amd.launcher import use_mode
+    return use_mode(backbone, mode)
 
 
 def tune_gemms(enable: bool) -> None:

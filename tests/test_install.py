@@ -77,3 +77,40 @@ def test_patch_tokens_equal_the_convolution():
     assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5)
     overlap = torch.nn.Conv2d(3, 8, 4, 2)
     assert torch.equal(patch_tokens(overlap, x), overlap(x).flatten(2).transpose(1, 2))
+
+
+def test_install_for_mode_explicit_arguments():
+    """Mode, sparsity and structural allocation as explicit arguments: the
+    per-layer ratios of allocation_settings on the backbone's layer-wise
+    installer; dense leaves the model unpatched."""
+    from vasc_amd import launcher
+    agg = Aggregator(dim=128, depth=24, num_heads=2, mlp_ratio=2.0)
+    agg, store, settings = install.install_for_mode(agg, "vggt", "vasc", 0.75, verbose=False)
+    assert settings["applied"] and settings["layer_sparsities"] == launcher.layer_sparsity("vggt", 0.75, "paper")
+    assert [b.attn.forward.__func__.keywords["sparse_ratio"] for b in agg.global_blocks] == settings["layer_sparsities"]
+    agg2, store2, s2 = install.install_for_mode(Aggregator(dim=128, depth=24, num_heads=2, mlp_ratio=2.0), "vggt",
+                                                "vasc", 0.75, structural_allocation=False, verbose=False)
+    assert not s2["applied"] and {b.attn.forward.__func__.keywords["sparse_ratio"] for b in agg2.global_blocks} == {0.75}
+    dense = Aggregator(dim=128, depth=24, num_heads=2, mlp_ratio=2.0)
+    same, none, sd = install.install_for_mode(dense, "vggt", "dense", 0.75)
+    assert same is dense and none is None and sd["effective_policy"] == "dense"
+    assert not any(hasattr(b.attn, "_sparse_routing_state") for b in dense.global_blocks)
+    pi3, _, sp = install.install_for_mode(Pi3Decoder(dim=128, depth=36, num_heads=2, mlp_ratio=2.0), "pi3", "topk",
+                                          0.75, verbose=False)
+    glob = [blk for i, blk in enumerate(pi3.decoder) if i % 2]
+    assert [b.attn.forward.__func__.keywords["sparse_ratio"] for b in glob] == sp["layer_sparsities"]
+    with pytest.raises(ValueError):
+        install.install_for_mode(dense, "vggt", "sparse", 0.75)
+
+
+def test_use_mode_sets_and_restores_the_switches(monkeypatch):
+    import os
+    from vasc_amd import launcher
+    monkeypatch.setenv("SPARSE_VGGT_QK_PV_THRESHOLD", "7")
+    monkeypatch.setenv("SPARSE_VGGT_SOMETHING_ELSE", "1")
+    with launcher.use_mode("vggt", "vasc") as env:
+        now = {k: v for k, v in os.environ.items() if k.startswith("SPARSE_VGGT_")}
+        assert now == env == launcher.method_environment("vggt", "vasc")
+        assert launcher.routing_config().mode == "vasc" and launcher.routing_config().official_mask
+    after = {k: v for k, v in os.environ.items() if k.startswith("SPARSE_VGGT_")}
+    assert after == {"SPARSE_VGGT_QK_PV_THRESHOLD": "7", "SPARSE_VGGT_SOMETHING_ELSE": "1"}

@@ -123,3 +123,28 @@ def sparse_model_from_pi3(model, use_hilbert: bool = False, sparse_ratio: float 
     if verbose:
         print(f"Pi3 global layer sparsity: {ratios}")
     return model, store
+
+
+def install_for_mode(model, backbone: str, mode: str, sparsity: float, structural_allocation: bool | None = None,
+                     **kwargs):
+    """Mode, sparsity and structural allocation as explicit arguments, as
+    the reference's evaluators apply them (evaluate.py:35-52, 183-231): the
+    per-layer ratios of ``allocation_settings`` installed with the backbone's
+    layer-wise installer; ``dense`` leaves the model as it is (the unpatched
+    upstream model). The kernels read the mode's switches at call time, so
+    run the model inside ``launcher.use_mode(backbone, mode)``. Returns
+    ``(model, aux_output_store or None, settings)``."""
+    from .launcher import MODES, allocation_settings
+    if mode not in MODES:
+        raise ValueError(f"mode must be one of {MODES}")
+    settings = allocation_settings(backbone, mode, sparsity, structural_allocation)
+    if mode == "dense":
+        return model, None, settings
+    ratios = settings["layer_sparsities"]
+    if backbone == "vggt":
+        model, store = sparse_aggregator_from_vggt_layerwise(model, layer_sparsity_ratios=ratios, **kwargs)
+    elif backbone == "pi3":
+        model, store = sparse_model_from_pi3(model, sparse_ratio=sparsity, layer_sparsity_ratios=ratios, **kwargs)
+    else:
+        raise ValueError("backbone must be vggt or pi3")
+    return model, store, settings

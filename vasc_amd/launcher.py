@@ -13,6 +13,7 @@ from __future__ import annotations
 import json
 import math
 import os
+from contextlib import contextmanager
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -90,6 +91,24 @@ def method_environment(backbone: str, mode: str) -> dict:
     if backbone == "vggt" and mode != "dense":
         values["OFFICIAL_MASK"] = 1
     return {"SPARSE_VGGT_" + k: str(v) for k, v in values.items()}
+
+
+@contextmanager
+def use_mode(backbone: str, mode: str):
+    """The release mode as an explicit argument: inside the block the
+    process environment holds exactly the ``SPARSE_VGGT_*`` switches of
+    ``method_environment(backbone, mode)`` (the reference's evaluators export
+    them for the whole process, evaluate.py:55-80, 193-195); the previous
+    switches are restored on exit."""
+    env = method_environment(backbone, mode)
+    saved = {k: os.environ.pop(k) for k in list(os.environ) if k.startswith("SPARSE_VGGT_")}
+    os.environ.update(env)
+    try:
+        yield env
+    finally:
+        for k in [k for k in os.environ if k.startswith("SPARSE_VGGT_")]:
+            del os.environ[k]
+        os.environ.update(saved)
 
 
 _TRUE = {"1", "true", "yes", "on"}
