@@ -139,12 +139,12 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
         attn_pooled = ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(hd))
     else:
         attn_pooled = predict_attention(q_patch, k_re[:, :, :n_patch], pool_mode=pool_mode)
-    x_patch, _, sparsity = sparse_global_attention(
+    tokens_out, _, sparsity = sparse_global_attention(
         q_patch, q_special, k_re, v_re, attn_pooled, sparse_ratio=sparse_ratio, cdf_threshold=cdf_threshold,
         layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch,
         want_sparsity=aux_output_store is not None, _innovation=innovation, token_layout=(N, P, S), **research)
     if aux_output_store is not None:
         aux_output_store["sparsity"] = sparsity
-    out = self.proj(x_patch.to(x.dtype))  # already in frame-major token order
+    out = self.proj(tokens_out.to(x.dtype))  # already in frame-major token order
     drop = getattr(self, "proj_drop", None)
     return drop(out) if drop is not None else out
