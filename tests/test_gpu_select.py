@@ -183,6 +183,12 @@ def test_vasc_c2_shape_chain():
     _run_chain(518, 259, 16, 3, topk=129, force_last=False, sink=3, peak=2.0, seed=2)
 
 
+def test_vasc_c4_shape_two_layers():
+    """Config 4 shape (Pi3, 64 frames): H=16, 518 x 1036 blocks, 5 sink blocks,
+    the structural budget of its non-favoured layers (233 blocks)."""
+    _run_chain(1036, 518, 16, 2, topk=233, force_last=False, sink=5, peak=2.0, seed=4)
+
+
 def test_vasc_c3_shape_two_layers():
     """Config 3 shape: H=16, 1036 x 2072 blocks at s=0.875 structural (224 blocks)."""
     _run_chain(2072, 1036, 16, 2, topk=224, force_last=False, sink=10, peak=2.0, seed=3)
