@@ -140,6 +140,20 @@ def test_host_only_queries_and_argument_errors():
                            None, None, f(1e-6), 0, None, None, f(1e-6), 0, None, 0, 2, None, None, 0,
                            None, None, None, None, None)
     assert rc == 2 and b"head_dim" in lib.vasc_last_error()
+    # v may be absent when v_out is (q and k only); k_out may not
+    fake = ctypes.c_void_p(256)  # aligned, never dereferenced: validation stops first
+    rc = lib.vasc_pack_qkv(fake, 0, 3072, 64, fake, 0, 3072, 64, None, 0, 0, 0, 1, 16, 2, 1041, 5, 64,
+                           None, None, f(1e-6), 0, None, None, f(1e-6), 0, None, 0, 2, None, None, 0,
+                           fake, fake, None, None, None)
+    assert rc == 1 and b"k_out is required" in lib.vasc_last_error()
+    rc = lib.vasc_pack_qkv(fake, 0, 3072, 64, fake, 0, 3072, 64, None, 0, 0, 0, 1, 16, 2, 1041, 5, 64,
+                           None, None, f(1e-6), 0, None, None, f(1e-6), 0, None, 0, 2, None, None, 0,
+                           None, fake, fake, None, None)
+    assert rc == 1 and b"q_patch is required" in lib.vasc_last_error()
+    rc = lib.vasc_pack_qkv(fake, 0, 3072, 64, fake, 0, 3072, 64, None, 0, 3072, 64, 1, 16, 2, 1041, 5, 64,
+                           None, None, f(1e-6), 0, None, None, f(1e-6), 0, None, 0, 2, None, None, 0,
+                           fake, fake, fake, fake, None)
+    assert rc == 1 and b"v is NULL" in lib.vasc_last_error()
     rc = lib.vasc_restore_tokens(None, 0, 0, 8, None, 0, 0, 8, 1, 16, 2, 1041, 5, 64, None, None)
     assert rc == 1 and b"out must be" in lib.vasc_last_error()
     rc = lib.vasc_restore_tokens(None, 0, 0, 8, None, 0, 0, 8, 1, 16, 2, 4, 5, 64, None, None)
