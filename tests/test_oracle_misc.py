@@ -205,3 +205,39 @@ def test_max_pool_blocks_matches_torch():
         ref = F.max_pool1d(x.reshape(6, T, 64).transpose(1, 2), blk, ceil_mode=True).transpose(1, 2)
         got = OP.max_pool_blocks(x.numpy(), blk)
         assert np.array_equal(got, ref.reshape(2, 3, -1, 64).numpy())
+
+
+def test_prob_bound_admits_rounding_flips_and_rejects_larger_errors():
+    """The pooled-probability tolerance: moving any logit by one bf16 step
+    (what a float32 dot product landing on the other side of a rounding
+    boundary does) stays inside the bound; a torch float32 matmul with its
+    own bf16 roundings stays inside; four steps on one logit, or a softmax
+    of a transposed key set, does not."""
+    rng = np.random.default_rng(5)
+    pq = OP.bf16_round((rng.standard_normal((1, 2, 20, 64)) * 4).astype(np.float32))
+    pk = OP.bf16_round((rng.standard_normal((1, 2, 40, 64)) * 4).astype(np.float32))
+    logits = OP.pooled_logits(pq, pk)
+    ref = OP.softmax(logits)
+    assert not OP.prob_outside_bound(ref, pq, pk).any()
+    # one bf16 step on the true value's side (below a power of two the gap is half the one above)
+    step = OP.bf16_spacing(np.abs(logits) * (1 - 2.0 ** -10)).astype(np.float32)
+    flip = np.where(rng.random(logits.shape) < 0.5, -1, 1).astype(np.float32)
+    assert not OP.prob_outside_bound(OP.softmax(logits + flip * step), pq, pk).any()
+    # the same predictor computed by torch in float32 with the autocast roundings
+    dots = torch.from_numpy(pq) @ torch.from_numpy(pk).transpose(-1, -2)
+    tl = dots.to(torch.bfloat16).float().mul(0.125).to(torch.bfloat16).float().softmax(-1).numpy()
+    assert not OP.prob_outside_bound(tl, pq, pk).any()
+    # a planted error of four steps on each row's largest logit is caught on every row
+    j = logits.argmax(-1)
+    bad = logits.copy()
+    np.put_along_axis(bad, j[..., None], np.take_along_axis(logits + 4 * step, j[..., None], -1), -1)
+    out = OP.prob_outside_bound(OP.softmax(bad), pq, pk)
+    assert out.any(-1).all()
+    # so is a predictor that pairs the queries with the wrong keys
+    assert OP.prob_outside_bound(OP.softmax(OP.pooled_logits(pq, pk[:, ::-1])), pq, pk).any()
+
+
+def test_bf16_spacing_is_the_gap_between_neighbours():
+    x = torch.tensor([1.0, 1.5, 2.0, 3.0, 0.01, 100.0, -7.0], dtype=torch.bfloat16)
+    nxt = torch.nextafter(x.abs(), torch.tensor(float("inf"), dtype=torch.bfloat16))
+    assert np.array_equal(OP.bf16_spacing(x.float().numpy()), (nxt.float() - x.abs().float()).numpy())
