@@ -1,8 +1,9 @@
 """VGGT/Pi3-shaped aggregators on the HIP kernels.
 
 * dense forward vs a float32 torch restatement of the same blocks (SDPA,
-  LayerNorm, rotary embedding in torch): max-abs <= 3e-2 * max|ref| + 3e-2
-  (bf16 weights and activations against float32);
+  LayerNorm, rotary embedding in torch), element by element:
+  |out - ref| <= 3e-2 * |ref| + 3e-2 * rms(ref) (bf16 activations against
+  float32 on the same bf16 weights);
 * the sparse install at sparsity 0 keeps every block and matches the dense
   forward (same tolerance);
 * VASC mode: the ledger is cleared at the start of a forward and settled
@@ -59,6 +60,18 @@ def _list_mask(index, count, n_patch, n_total):
     return bm[..., :kbt].repeat_interleave(128, 2)[:, :, :n_patch].repeat_interleave(64, 3)[..., :n_total]
 
 
+def _chunked_attention(q, k, v, rows: int = 2048):
+    """float32 softmax attention over query chunks (a full score matrix of a
+    33 312-token layer would take 71 GB)."""
+    kt = k.transpose(-1, -2).contiguous()
+    out = torch.empty_like(q)
+    scale = q.shape[-1] ** -0.5
+    for i in range(0, q.shape[2], rows):
+        s = torch.matmul(q[:, :, i:i + rows].contiguous(), kt) * scale
+        out[:, :, i:i + rows] = torch.matmul(s.softmax(-1), v)
+    return out
+
+
 def _ref_attention(attn, x, pos, sparse=None):
     """float32 attention of one block; ``sparse = (N, P, S, index, count)``
     restricts the patch queries of a global layer to their listed blocks
@@ -71,7 +84,9 @@ def _ref_attention(attn, x, pos, sparse=None):
     q = F.layer_norm(q, (D,), attn.q_norm.weight.float(), attn.q_norm.bias.float(), attn.q_norm.eps)
     k = F.layer_norm(k, (D,), attn.k_norm.weight.float(), attn.k_norm.bias.float(), attn.k_norm.eps)
     q, k = attn.rope(q, pos), attn.rope(k, pos)
-    if sparse is None:
+    if sparse is None and T > 8192:
+        o = _chunked_attention(q, k, v)
+    elif sparse is None:
         o = F.scaled_dot_product_attention(q, k, v)
     else:
         N, P, S, index, count = sparse
@@ -174,9 +189,17 @@ def _oracle_chain(layers, n_patch, n_total, ratios, mode, official):
             assert np.array_equal(a, idx.reshape(-1, idx.shape[-1])[r, :n]), f"layer {li}: row {r}"
 
 
-def _close(out, ref):
-    err = (out.float() - ref).abs().max().item()
-    assert err <= 3e-2 * ref.abs().max().item() + 3e-2, (err, ref.abs().max().item())
+def _close(out, ref, rtol: float = 3e-2, atol: float = 3e-2):
+    """Element-wise |out - ref| <= rtol*|ref| + atol*rms(ref): a few bf16
+    roundings (2^-8 relative each) per block, on every element, with the
+    row-independent floor for elements near zero."""
+    out, ref = out.float(), ref.float()
+    rms = ref.square().mean().sqrt().item()
+    err = (out - ref).abs()
+    worst = (err / (rtol * ref.abs() + atol * rms)).max().item()
+    print(f"max-abs {err.max().item():.3e}, mean-abs {err.mean().item():.3e}, rms(ref) {rms:.3e}, "
+          f"worst error / bound {worst:.3f}")
+    assert worst <= 1.0, worst
 
 
 def _images(N=3, H=70, W=84, seed=1):
@@ -295,3 +318,40 @@ def test_pi3_decoder_sparse_matches_torch_float32_on_its_lists(mode, dim, monkey
         ref = _ref_pi3(model, images, rec.layers)
     _close(sparse, ref)
 
+
+
+def test_c2_width_and_length_blocks():
+    """Four frame and four global blocks at config 2's width and sequence
+    length (dim 1024, 16 heads, MLP 4096, 32 frames at 392x518: 33 312 global
+    tokens): the dense bf16 forward against the float32 restatement; the
+    sparse install at sparsity 0 against the dense forward; the vasc forward
+    at the structural profile's first four ratios finite and bit-identical
+    over two forwards (the ledger is cleared per forward)."""
+    images = _images(N=32, H=392, W=518, seed=2)
+    agg = _model(Aggregator, dim=1024, depth=4, num_heads=16, mlp_ratio=4.0, intermediate_layer_idx=(3,))
+    agg = agg.to(torch.bfloat16)
+    with torch.no_grad():
+        dense, _ = agg(images)
+        ref = _ref_aggregator(agg, images)
+        # 16 residual updates of a 1024-wide stream (the small cases above run 4 to 12)
+        _close(dense[-1][..., 1024:], ref, rtol=5e-2, atol=5e-2)
+        del ref
+        with _Env("vggt", "topk"):
+            install.sparse_aggregator_from_vggt(agg, sparse_ratio=0.0, verbose=False)
+            zero, _ = agg(images)
+        _close(zero[-1], dense[-1], rtol=1e-2, atol=1e-2)
+    del agg, zero
+    agg = _model(Aggregator, dim=1024, depth=4, num_heads=16, mlp_ratio=4.0, intermediate_layer_idx=(3,))
+    agg = agg.to(torch.bfloat16)
+    ratios = launcher.layer_sparsity("vggt", 0.75, "paper")[:4]
+    with torch.no_grad(), _Env("vggt", "vasc"):
+        _, store = install.sparse_aggregator_from_vggt_layerwise(agg, layer_sparsity_ratios=ratios, aux_output=True,
+                                                                verbose=False)
+        a, _ = agg(images)
+        b, _ = agg(images)
+    assert torch.isfinite(a[-1]).all()
+    assert torch.equal(a[-1], b[-1])
+    for i in range(4):  # 120 of 518 patch blocks plus 3 sink blocks per row
+        assert abs(float(store[i]["sparsity"]) - (1 - 123 / 521)) < 1e-6, store[i]["sparsity"]
+    d = (a[-1].float() - dense[-1].float()).abs()
+    print(f"vasc vs dense after 4 global blocks: max-abs {d.max().item():.3e} mean-abs {d.mean().item():.3e}")
