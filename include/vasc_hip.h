@@ -373,7 +373,8 @@ int vasc_dense_attn_fwd(const uint16_t *q, int64_t q_sb, int64_t q_sh,
  *   k = qkv + H*d, v = qkv + 2*H*d with st = 3*H*d, sh = d.
  * q_norm / k_norm != 0: LayerNorm over the d features of each (token, head)
  *   with optional weight and bias [d] (NULL: 1 / 0) and eps, before the
- *   rotary embedding.
+ *   rotary embedding; 1: weight and bias are float32, 2: bfloat16 (the
+ *   parameters of a bf16 model are read as they are, no converted copy).
  * pos != NULL: 2D rotary embedding of q and k. Token (b,t) has the integer
  *   row / column position pos[b*pos_sb + t*pos_st + 0 / 1]; features
  *   [0, d/2) rotate with the row, [d/2, d) with the column; inside a half,
@@ -395,9 +396,9 @@ int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                   const uint16_t *k, int64_t k_sb, int64_t k_st, int64_t k_sh,
                   const uint16_t *v, int64_t v_sb, int64_t v_st, int64_t v_sh,
                   int64_t B, int64_t H, int64_t N, int64_t P, int64_t S,
-                  int64_t d, const float *q_norm_w, const float *q_norm_b,
-                  float q_eps, int32_t q_norm, const float *k_norm_w,
-                  const float *k_norm_b, float k_eps, int32_t k_norm,
+                  int64_t d, const void *q_norm_w, const void *q_norm_b,
+                  float q_eps, int32_t q_norm, const void *k_norm_w,
+                  const void *k_norm_b, float k_eps, int32_t k_norm,
                   const int32_t *pos, int64_t pos_sb, int64_t pos_st,
                   const float *rope_cos, const float *rope_sin, int64_t rope_n,
                   uint16_t *q_patch, uint16_t *q_special, uint16_t *k_out,

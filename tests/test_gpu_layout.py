@@ -346,3 +346,31 @@ def test_global_layer_vasc_chain_matches_oracle(backbone, monkeypatch):
         err = (out.float() - ref).abs()
         assert err.max() < 6e-2 and err.mean() < 6e-3, (layer, err.max().item(), err.mean().item())
     assert "cosa_value_risk_pair_debt" in routing_state
+
+
+def test_pack_norm_parameters_bf16_and_updated_through_data():
+    """bf16 LayerNorm parameters are read as they are (identical to their
+    float32 values), and a parameter rewritten through ``.data`` (which
+    leaves its version counter alone) is seen by the next call."""
+    from vasc_amd import ops
+    N, P, S, H, D = 2, 70, 5, 3, 64
+    x = _bf16((1, N * P, 3 * H * D), 17, 2.0).cuda().view(1, N * P, 3, H, D)
+    g = torch.Generator().manual_seed(18)
+    w = torch.nn.Parameter((1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda())
+    b = torch.nn.Parameter((0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda())
+
+    def run(wt, bt):
+        return ops.pack_qkv(x[:, :, 0], x[:, :, 1], x[:, :, 2], N, P, S, q_norm=(wt, bt, 1e-6),
+                            k_norm=(wt, None, 1e-6))
+
+    first = run(w, b)
+    as_f32 = run(w.float(), b.float())
+    for a, c in zip(first, as_f32):
+        assert torch.equal(a.view(torch.int16), c.view(torch.int16))
+    new_w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+    w.data.copy_(new_w)
+    second = run(w, b)
+    fresh = run(new_w.clone(), b.detach().clone())
+    for a, c in zip(second, fresh):
+        assert torch.equal(a.view(torch.int16), c.view(torch.int16))
+    assert not torch.equal(first[0].view(torch.int16), second[0].view(torch.int16))

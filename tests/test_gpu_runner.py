@@ -65,3 +65,33 @@ def test_residual_norm_argument_errors():
     with pytest.raises(_lib.VascArgumentError):
         _lib.call("vasc_residual_norm", x.data_ptr(), 1024, x.data_ptr(), 1024, None, None, None, 1e-6, None, 1024,
                   None, 1024, 4, 1024, None)
+
+
+def test_residual_norm_rejects_fp32_parameters():
+    x = torch.zeros(4, 1024, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="bf16"):
+        ops.residual_norm(x, x, torch.ones(1024, device="cuda"))
+
+
+def test_block_with_fp32_parameters_takes_the_torch_ops():
+    """A bf16 activation stream through a block whose LayerScale and
+    LayerNorm parameters are float32 (an fp32 model under autocast): the
+    block must not round the parameters to bf16; it matches the same block
+    run as torch ops, and a parameter rewritten through ``.data`` is used."""
+    from vasc_amd.aggregator import Block
+    torch.manual_seed(3)
+    blk = Block(512, 8, 2.0).cuda()
+    with torch.no_grad():
+        blk.ls1.gamma.normal_(0.3, 0.1)
+        blk.ls2.gamma.normal_(0.3, 0.1)
+        blk.norm2.weight.normal_(1.0, 0.1)
+    x = torch.randn(1, 300, 512, device="cuda").to(torch.bfloat16)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        out = blk(x)
+        h = blk.attn(blk.norm1(x))
+        ref = x + blk.ls1(h)
+        ref = ref + blk.ls2(blk.mlp(blk.norm2(ref)))
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        blk.ls2.gamma.data.copy_(torch.zeros(512))
+        out2 = blk(x)
+        assert torch.equal(out2.view(torch.int16), (x + blk.ls1(h)).to(out2.dtype).view(torch.int16))

@@ -180,7 +180,7 @@ class Block(nn.Module):
         ``vasc_residual_norm`` pass, rounded as the separate torch ops."""
         h = self.norm1(x) if normed is None else normed
         a = self.attn(h, pos=pos)
-        if not _fused_residual(x, a):
+        if not _fused_residual(x, a, self, next_norm):
             x = x + self.ls1(a)
             x = x + self.ls2(self.mlp(self.norm2(x)))
             return x if next_norm is None else (x, next_norm(x))
@@ -189,9 +189,17 @@ class Block(nn.Module):
         return x if next_norm is None else (x, nxt)
 
 
-def _fused_residual(x: torch.Tensor, y: torch.Tensor) -> bool:
-    return (x.is_cuda and x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16 and x.shape == y.shape
-            and x.shape[-1] in (512, 1024, 1536, 2048))
+def _fused_residual(x: torch.Tensor, y: torch.Tensor, blk: "Block", next_norm: nn.LayerNorm | None) -> bool:
+    """The fused pass rounds as torch's bf16 ops do on bf16 activations and
+    bf16 parameters; anything else (fp32 parameters under autocast, where
+    torch promotes the products and the LayerNorm to fp32) takes the torch ops."""
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16 and x.shape == y.shape
+            and x.shape[-1] in (512, 1024, 1536, 2048)):
+        return False
+    params = [blk.ls1.gamma, blk.ls2.gamma, blk.norm2.weight, blk.norm2.bias]
+    if next_norm is not None:
+        params += [next_norm.weight, next_norm.bias]
+    return all(p is None or p.dtype == torch.bfloat16 for p in params)
 
 
 def _ln(norm: nn.LayerNorm):

@@ -46,9 +46,9 @@ struct PackParams {
   const uint16_t *src[3];       // q, k, v: element (b, t, h, d) at src + b*sb + t*st + h*sh + d
   int64_t sb[3], st[3], sh[3];
   int32_t H, N, P, S;           // T = N * P frame-major tokens
-  const float *norm_w[2], *norm_b[2];
+  const void *norm_w[2], *norm_b[2];
   float eps[2];
-  int32_t norm[2];              // LayerNorm of q (0) and k (1)
+  int32_t norm[2];              // LayerNorm of q (0) and k (1): 0 none, 1 fp32 parameters, 2 bf16 parameters
   const int32_t *pos;           // (row, column) position of token (b, t) at pos + b*pos_sb + t*pos_st
   int64_t pos_sb, pos_st;
   const float *rope_cos, *rope_sin;  // [rope_n, 16]: cos/sin of position p times frequency i
@@ -83,8 +83,11 @@ __global__ __launch_bounds__(kThreads) void pack_qkv_kernel(const PackParams p) 
   if (any_norm) {
     const int which = tid >> 7, wb = (tid >> 6) & 1, f = tid & 63;
     // a tensor without the norm may pass any pointer: read only the normed one's
-    const float *src = !p.norm[which] ? nullptr : (wb == 0 ? p.norm_w[which] : p.norm_b[which]);
-    reinterpret_cast<float *>(nrm[which][wb])[f] = src ? src[f] : (wb == 0 ? 1.f : 0.f);
+    const void *src = !p.norm[which] ? nullptr : (wb == 0 ? p.norm_w[which] : p.norm_b[which]);
+    float val = wb == 0 ? 1.f : 0.f;
+    if (src)
+      val = p.norm[which] == 2 ? bf16_to_f32(static_cast<const uint16_t *>(src)[f]) : static_cast<const float *>(src)[f];
+    reinterpret_cast<float *>(nrm[which][wb])[f] = val;
   }
   bool ok[kPackPasses];
   int32_t tk[kPackPasses], pt[kPackPasses], hd[kPackPasses];
@@ -224,8 +227,8 @@ int check_src(const char *name, const void *ptr, int64_t sb, int64_t st, int64_t
 extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int64_t q_sh, const uint16_t *k,
                              int64_t k_sb, int64_t k_st, int64_t k_sh, const uint16_t *v, int64_t v_sb,
                              int64_t v_st, int64_t v_sh, int64_t B, int64_t H, int64_t N, int64_t P, int64_t S,
-                             int64_t d, const float *q_norm_w, const float *q_norm_b, float q_eps,
-                             int32_t q_norm, const float *k_norm_w, const float *k_norm_b, float k_eps,
+                             int64_t d, const void *q_norm_w, const void *q_norm_b, float q_eps,
+                             int32_t q_norm, const void *k_norm_w, const void *k_norm_b, float k_eps,
                              int32_t k_norm, const int32_t *pos, int64_t pos_sb, int64_t pos_st,
                              const float *rope_cos, const float *rope_sin, int64_t rope_n, uint16_t *q_patch,
                              uint16_t *q_special, uint16_t *k_out, uint16_t *v_out, void *stream) {
@@ -245,6 +248,8 @@ extern "C" int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int6
   for (const void *o : {static_cast<const void *>(q_patch), static_cast<const void *>(q_special),
                         static_cast<const void *>(k_out), static_cast<const void *>(v_out)})
     VASC_REQUIRE((reinterpret_cast<uintptr_t>(o) & 15) == 0, "outputs must be 16-byte aligned");
+  VASC_REQUIRE(q_norm >= 0 && q_norm <= 2 && k_norm >= 0 && k_norm <= 2,
+               "q_norm / k_norm must be 0 (none), 1 (fp32 parameters) or 2 (bf16 parameters)");
   VASC_REQUIRE(q_norm == 0 || q_eps >= 0.f, "q_eps must be non-negative");
   VASC_REQUIRE(k_norm == 0 || k_eps >= 0.f, "k_eps must be non-negative");
   if (pos) {

@@ -397,26 +397,17 @@ def _btht(t: torch.Tensor, name: str) -> tuple:
     return t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)
 
 
-_PARAM_CACHE: dict = {}
-
-
-def _param_as(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """A small parameter as a contiguous ``dtype`` tensor on its device,
-    converted once per (storage, version): repeated layer calls then launch
-    no conversion kernels. The entry keeps the source alive, so its address
-    cannot be reused while cached; an in-place update bumps the version."""
+def _param(t: torch.Tensor, name: str, numel: int, dtypes: tuple) -> torch.Tensor:
+    """A [numel] parameter as a contiguous device tensor of one of ``dtypes``
+    (converted to the first when it is none of them). Nothing is cached: the
+    kernel reads the parameter's current values on every call."""
     t = t.detach()
-    if t.dtype == dtype and t.is_contiguous():
-        return t
-    key = (t.data_ptr(), t._version, t.dtype, dtype, tuple(t.shape), tuple(t.stride()))
-    hit = _PARAM_CACHE.get(key)
-    if hit is not None:
-        return hit[1]
-    if len(_PARAM_CACHE) > 4096:
-        _PARAM_CACHE.clear()
-    conv = t.to(dtype).contiguous()
-    _PARAM_CACHE[key] = (t, conv)
-    return conv
+    _dev(t, name)
+    if t.numel() != numel:
+        raise ValueError(f"{name} must hold {numel} values")
+    if t.dtype not in dtypes:
+        t = t.to(dtypes[0])
+    return t.contiguous()
 
 
 def residual_norm(x: torch.Tensor, y: torch.Tensor, gamma: torch.Tensor | None = None, norm=None):
@@ -444,10 +435,9 @@ def residual_norm(x: torch.Tensor, y: torch.Tensor, gamma: torch.Tensor | None =
     def param(t, name):
         if t is None:
             return None
-        if t.numel() != dim:
-            raise ValueError(f"{name} must hold {dim} values")
-        t = _param_as(t, torch.bfloat16)
-        _dev(t, name)
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bf16: the pass rounds as torch's bf16 ops on bf16 parameters")
+        t = _param(t, name, dim, (torch.bfloat16,))
         keep.append(t)
         return t.data_ptr()
 
@@ -487,18 +477,18 @@ def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, frames: i
         if nrm is None:
             return (None, None, 0.0, 0)
         w, b, eps = nrm
+        given = [t for t in (w, b) if t is not None]
+        # both parameters in one dtype the kernel reads directly: bf16 (2) or float32 (1)
+        kind = 2 if given and all(t.dtype == torch.bfloat16 for t in given) else 1
         out = []
         for t in (w, b):
             if t is None:
                 out.append(None)
             else:
-                if t.numel() != D:
-                    raise ValueError(f"{name} parameters must hold {D} values")
-                t = _param_as(t, torch.float32)
-                _dev(t, name)
+                t = _param(t, f"{name} parameters", D, (torch.bfloat16,) if kind == 2 else (torch.float32,))
                 keep.append(t)
                 out.append(t.data_ptr())
-        return (out[0], out[1], float(eps), 1)
+        return (out[0], out[1], float(eps), kind)
 
     rope = (None, 0, 2, None, None, 0)
     if pos is not None:
