@@ -319,15 +319,28 @@ def test_plain_launch_with_a_stand_in_evaluator_and_no_overwrite(tmp_path):
     (tmp_path / "checkpoints/vggt/model.pt").touch()
     for folder in ("data/nrgbd", "external/StreamVGGT/src/eval/mv_recon", "external/vggt/vggt", "evaluation"):
         (tmp_path / folder).mkdir(parents=True)
+    # the stand-in imports what the reference's evaluator imports (eval_7scenes_sparse_vggt.py:939-941,
+    # 1115-1118) and records which files those names resolve to
     (tmp_path / "evaluation/eval_7scenes_sparse_vggt.py").write_text(
         "import json, os, pathlib, sys\n"
+        "import sparse_vggt\n"
+        "from sparse_vggt.utils import sparse_wrapper\n"
+        "from sparse_vggt.models.vggt import sparse_aggregator_from_vggt\n"
+        "from sparse_vggt.models.vggt_layerwise import sparse_aggregator_from_vggt_layerwise\n"
+        "import vasc_amd.install, vasc_amd.sparse_wrapper\n"
         "path = pathlib.Path(sys.argv[sys.argv.index('--metrics_json') + 1])\n"
-        "path.write_text(json.dumps({'stand_in': True, 'mode': os.environ['SPARSE_VGGT_COSA_VALUE_RISK_PAIR_DEBT']}))\n"
+        "path.write_text(json.dumps({'stand_in': True, 'mode': os.environ['SPARSE_VGGT_COSA_VALUE_RISK_PAIR_DEBT'],\n"
+        "    'wrapper': sparse_wrapper.__file__,\n"
+        "    'same_wrapper': sparse_wrapper is vasc_amd.sparse_wrapper,\n"
+        "    'same_installers': sparse_aggregator_from_vggt is vasc_amd.install.sparse_aggregator_from_vggt\n"
+        "        and sparse_aggregator_from_vggt_layerwise is vasc_amd.install.sparse_aggregator_from_vggt_layerwise}))\n"
         "print('stand-in evaluation finished')\n", encoding="utf-8")
     with patch.object(run, "ROOT", tmp_path), redirect_stdout(io.StringIO()):
         run.main(["--evaluation-root", str(tmp_path / "evaluation")])
     out = tmp_path / "outputs/result"
-    assert json.loads((out / "metrics.json").read_text()) == {"stand_in": True, "mode": "1"}
+    metrics = json.loads((out / "metrics.json").read_text())
+    assert metrics == {"stand_in": True, "mode": "1", "wrapper": str(run.ROOT / "vasc_amd" / "sparse_wrapper.py"),
+                       "same_wrapper": True, "same_installers": True}
     assert "stand-in evaluation finished" in (out / "run.log").read_text()
     launch = json.loads((out / "launch.json").read_text())
     assert launch["allocation"]["applied"]
@@ -335,3 +348,46 @@ def test_plain_launch_with_a_stand_in_evaluator_and_no_overwrite(tmp_path):
     with patch.object(run, "ROOT", tmp_path), redirect_stderr(io.StringIO()), pytest.raises(SystemExit):
         run.main(["--evaluation-root", str(tmp_path / "evaluation")])
     assert {p.name: p.read_bytes() for p in out.iterdir()} == snapshot
+
+
+def test_pi3_launch_is_refused_before_anything_runs(tmp_path):
+    """The Pi3 evaluator imports the reconstruction protocol this build does
+    not ship (eval_pi3_sparse.py:251): a real launch stops with that reason
+    and leaves no output folder; its dry run still prints the command."""
+    config = tmp_path / "configs/local.json"
+    config.parent.mkdir()
+    config.write_text(json.dumps({**EXAMPLE, "backbone": "pi3", "output": "outputs/pi3",
+                                  "runtime_root": str(run.ROOT)}))
+    (tmp_path / "checkpoints/vggt").mkdir(parents=True)
+    (tmp_path / "checkpoints/vggt/model.pt").touch()
+    for folder in ("data/nrgbd", "external/StreamVGGT/src/eval/mv_recon", "external/vggt/vggt", "external/Pi3/pi3",
+                   "evaluation"):
+        (tmp_path / folder).mkdir(parents=True)
+    (tmp_path / "evaluation/eval_pi3_sparse.py").write_text("raise SystemExit(3)\n")
+    err = io.StringIO()
+    with patch.object(run, "ROOT", tmp_path), redirect_stderr(err), pytest.raises(SystemExit):
+        run.main(["--evaluation-root", str(tmp_path / "evaluation")])
+    assert "pi3_reconstruction" in err.getvalue()
+    assert not (tmp_path / "outputs/pi3").exists()
+    out = io.StringIO()
+    with patch.object(run, "ROOT", tmp_path), redirect_stdout(out):
+        run.main(["--evaluation-root", str(tmp_path / "evaluation"), "--dry-run"])
+    record = json.loads(out.getvalue())
+    assert record["command"][1].endswith("eval_pi3_sparse.py") and _opt(record["command"], "--max_points") == "200000"
+    assert record["environment"]["PYTHONPATH"].split(os.pathsep)[0] == str(run.ROOT / "vasc_amd" / "compat")
+
+
+def test_settings_table_drives_parser_and_config():
+    """Every setting is both a config key and a command-line option, with
+    the same default the parser reports."""
+    cli = run.parser({"backbone": "vggt", "dataset": "nrgbd", "weights": Path("w"), "data_root": Path("d")})
+    ns = cli.parse_args([])
+    for s in run.SETTINGS:
+        assert hasattr(ns, s.key)
+        if s.kind == "path" and s.default is not None:
+            assert getattr(ns, s.key) == run.ROOT / s.default
+        elif s.key not in ("backbone", "dataset", "weights", "data_root"):
+            assert getattr(ns, s.key) == s.default
+    assert {s.key for s in run.SETTINGS} == set(json.loads(run.EXAMPLE.read_text())) | {
+        "runtime_root", "evaluation_root", "output", "output_root", "stride", "scene", "sequence", "frame_limit",
+        "warmup", "repeats", "pose_only"}

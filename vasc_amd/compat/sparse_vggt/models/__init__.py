@@ -1,0 +1,1 @@
+"""Shim subpackage (see ``sparse_vggt/__init__.py``)."""
