@@ -105,13 +105,14 @@ def test_host_only_queries_and_argument_errors():
     lib = _lib.load()
     # per row: total, row pair sum, capacity (fp32/int32); per pair: admitted
     # debt, (innovation, debt) pair, service counts; per 32-row chunk and
-    # pair: a float64 partial of the arrival mean; per head: 3 gate partials.
+    # pair: a float64 partial of the arrival mean; per head: 3 gate partials;
+    # per row: the select pass's fast-path flag.
     def al(x):
         return (x + 255) // 256 * 256
     BH, Q, K = 16, 259, 518
     P, chunks = (K + 1) // 2, -(-Q // 32)
     expect = 3 * al(BH * Q * 4) + al(BH * P * 4) + al(BH * P * 8) + al(BH * chunks * P * 8) + al(BH * 3 * 8) \
-        + al(BH * P * 4)
+        + al(BH * P * 4) + al(BH * Q * 4)
     assert lib.vasc_select_workspace_size(1, BH, Q, K) == expect
     assert lib.vasc_select_workspace_size(0, 16, 259, 518) == 0
     # result regions: row totals, row pair sums, capacities, then the admitted debt

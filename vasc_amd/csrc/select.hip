@@ -90,6 +90,7 @@ struct SelectParams {
   float2 *ia;  // (innovation, admitted debt) per pair, for the select pass
   double *part, *gate_part;
   int32_t *cap, *counts;
+  int32_t *flags;  // per row: the select pass may take the fast path (register-row kernels)
   int64_t nchunks;
 };
 
@@ -328,145 +329,6 @@ __global__ __launch_bounds__(1024) void arrival_kernel(const SelectParams p, int
   }
 }
 
-// Arrival for rows of at most 64 * EPT key blocks, with the row in
-// registers instead of an LDS buffer: lane j loads elements j + 64 m (m <
-// EPT) with coalesced dword loads, which is exactly the lane order of the
-// canonical wave sums; several waves per SIMD hide the load latency. The
-// innovation of the head sits in LDS; the pair
-// partner A[k + 1] of an even lane comes from its right neighbour by DPP.
-// Rows, arithmetic and the float64 column partials (thread t: pairs t,
-// t + 64 kRowWaves, ... of the kRowWaves rows of a group, in row order) are
-// those of arrival_kernel.
-template <int EPT, int kRowWaves>
-__global__ __launch_bounds__(64 * kRowWaves) void arrival_reg_kernel(const SelectParams p) {
-  extern __shared__ __attribute__((aligned(16))) float alds[];
-  constexpr int kThreads = 64 * kRowWaves;
-  constexpr int kPairs = (64 * EPT / 2 + kThreads - 1) / kThreads;  // column partials per thread
-  const int P = static_cast<int>(p.P), K = static_cast<int>(p.K);
-  float *iota_s = alds;   // [P]
-  float *apair = alds + P;  // [kRowWaves][P]
-  const int64_t chunk = blockIdx.x, bh = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t q0 = chunk * kChunk;
-  const int nrows = static_cast<int>(p.Q - q0 < kChunk ? p.Q - q0 : kChunk);
-  for (int i = tid; i < P; i += kThreads) iota_s[i] = p.innovation[bh * P + i];
-  double part[kPairs];
-#pragma unroll
-  for (int i = 0; i < kPairs; ++i) part[i] = 0.0;
-  __syncthreads();
-
-  // The row is read through buffer resources rebased every 16 elements, so
-  // every offset is the lane's 4 * lane plus an immediate below 4096, and
-  // elements past the row end read as 0 (raw buffer range check against
-  // num_records) without touching memory.
-  auto load = [&](float (&x)[EPT], int r, int ln) {
-    const float *srow = p.score + (bh * p.Q + q0 + r) * p.K;
-#pragma unroll
-    for (int g = 0; g < (EPT + 15) / 16; ++g) {
-      const int left = K - 1024 * g;
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<float *>(srow + (left > 0 ? 1024 * g : 0)), 0, left > 0 ? 4 * left : 0, 0x00020000);
-#pragma unroll
-      for (int m = 16 * g; m < EPT && m < 16 * g + 16; ++m)
-        x[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 4 * ln + 256 * (m - 16 * g), 0, 0));
-    }
-  };
-  auto process = [&](float (&x)[EPT], int r, int ln) {
-    const int64_t row = bh * p.Q + q0 + r;
-    int cap;
-    if (p.row_cap) {
-      cap = p.row_cap[row];
-    } else {
-      cap = p.topk < 1 ? 1 : p.topk;
-      cap = cap > K ? K : cap;
-      if (p.force_last && cap < K) {
-        const uint32_t last = order_key(p.score[row * p.K + K - 1]);  // wave-uniform load
-        int beat = 0;
-#pragma unroll
-        for (int m = 0; m < EPT; ++m) {
-          const int k = ln + 64 * m;
-          const uint32_t kk = order_key(x[m]);
-          const bool in = k < K;
-          beat += in && ((kk > last) || (kk == last && k < K - 1));
-        }
-        cap += wave_sum_int(beat) >= cap ? 1 : 0;
-      }
-    }
-    // Elements past the row end become risk +0.0 and pair value +0.0: adding
-    // +0.0 to a sum that started at +0.0 leaves it bit-identical, so every
-    // element runs the same branch-free code.
-    double acc = 0.0;
-#pragma unroll
-    for (int m = 0; m < EPT; ++m) {
-      const int k = ln + 64 * m;
-      const bool in = k < K;
-      const float risk = clean_score(x[m]) * iota_s[(in ? k : K - 1) >> 1];
-      x[m] = in ? risk : 0.f;
-      acc = acc + static_cast<double>(x[m]);
-    }
-    const float total = static_cast<float>(wave_butterfly(acc));
-    const float scale = static_cast<float>(cap) / floor_tiny(total);
-    const bool live = total > 0.f;
-    const bool even = (ln & 1) == 0;
-    double racc = 0.0;
-    float *ap_row = apair + w * P;
-#pragma unroll
-    for (int m = 0; m < EPT; ++m) {
-      const int k = ln + 64 * m;
-      const bool in = k < K;
-      const float A = live && in ? clamp01(x[m] * scale) : 0.f;
-      // right neighbour inside the 16-lane row (even lanes never sit at a row end)
-      const float An = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(A), 0x101, 0xf, 0xf, false));
-      const float ap = (k + 1 < K) ? (A + An) / 2.0f : (A + 0.0f) / 1.0f;
-      // the summand is fixed before the store's branch, so the row sum stays
-      // one in-order chain instead of per-element doubles summed afterwards
-      float add = in && even ? ap : 0.f;
-      asm volatile("" : "+v"(add));
-      racc = racc + static_cast<double>(add);
-      asm volatile("" : "+v"(racc));
-      if (in && even) ap_row[k >> 1] = ap;
-    }
-    const float rowpair = static_cast<float>(wave_butterfly(racc));
-    if (ln == 0) {
-      p.total[row] = total;
-      p.rowpair[row] = rowpair;
-      p.cap[row] = cap;
-    }
-  };
-  auto accumulate = [&](int rows_here) {
-    int t = tid;
-    asm volatile("" : "+v"(t));  // addresses made here, not held across the row loop
-#pragma unroll
-    for (int i = 0; i < kPairs; ++i) {
-      const int pp = t + kThreads * i;
-      if (pp < P)
-        for (int rr = 0; rr < rows_here; ++rr) part[i] = part[i] + static_cast<double>(apair[rr * P + pp]);
-    }
-  };
-
-  float x[EPT];
-  for (int r0 = 0; r0 < nrows; r0 += kRowWaves) {
-    if (r0 + w < nrows) {
-      // an opaque copy of the lane index keeps the per-element offsets and
-      // row-end masks inside the loop instead of hoisted into registers
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-      load(x, r0 + w, ln);
-      process(x, r0 + w, ln);
-    }
-    __syncthreads();
-    accumulate(nrows - r0 < kRowWaves ? nrows - r0 : kRowWaves);
-    __syncthreads();
-  }
-  double *out = p.part + (bh * p.nchunks + chunk) * p.P;
-#pragma unroll
-  for (int i = 0; i < kPairs; ++i) {
-    const int pp = tid + kThreads * i;
-    if (pp < P) out[pp] = part[i];
-  }
-}
-
 // ------------------------------------------------------------------ head
 // Per head: ledger settlement, pending arrival (mean over rows), pair
 // capacity and admitted debt. Wave 0 of every workgroup recomputes the head's
@@ -598,6 +460,25 @@ __device__ __forceinline__ int rank_bin(const u32x4 &h, int suf, int lane, int r
   return bal ? __builtin_amdgcn_readlane(found, __builtin_ctzll(bal)) : -1;
 }
 
+// The r-th largest (1 <= r <= n) of n <= 64 keys, one per lane (lanes >= n
+// hold none), all inside [lo, lo + 2^bits): the largest t with at least r keys
+// >= t, built bit by bit from the top with ballot counts. Returns T and the
+// numbers of keys above it (gt) and equal to it (eq).
+__device__ __forceinline__ uint32_t rank_small(uint32_t mine, int n, int lane, uint32_t lo, int bits, int r, int &gt,
+                                               int &eq) {
+  const bool valid = lane < n;
+  const uint32_t v = valid ? mine - lo : 0u;
+  const uint64_t vm = __builtin_amdgcn_ballot_w64(valid);
+  uint32_t pre = 0;
+  for (int b = bits - 1; b >= 0; --b) {
+    const uint32_t t = pre | (1u << b);
+    if (__popcll(__builtin_amdgcn_ballot_w64(v >= t) & vm) >= r) pre = t;
+  }
+  gt = __popcll(__builtin_amdgcn_ballot_w64(v > pre) & vm);
+  eq = __popcll(__builtin_amdgcn_ballot_w64(v == pre) & vm);
+  return lo + pre;
+}
+
 // The c-th largest key (c >= 1) counting from the top of [kmin, kmax];
 // keys above kmax are counted first. Each level histograms the keys of the
 // current range into 256 bins of width 2^sh and takes the bin holding the
@@ -684,18 +565,10 @@ __device__ bool rank_keys(const uint32_t (&key)[EPT], int lane, uint32_t kmin, u
         if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
       wave_sync();
-      const uint32_t mine = lane < inb ? sbuf[lane] : 0u;
-      int gt = 0, eq = 0;
-      for (int jj = 0; jj < inb; ++jj) {
-        const uint32_t x = __builtin_amdgcn_readlane(mine, jj);
-        gt += x > mine;
-        eq += x == mine;
-      }
-      const bool isT = lane < inb && gt < need_b && need_b <= gt + eq;
-      const int Lt = __builtin_ctzll(__builtin_amdgcn_ballot_w64(isT));
-      need = need_b - __builtin_amdgcn_readlane(gt, Lt);
-      eqT = __builtin_amdgcn_readlane(eq, Lt);
-      T = __builtin_amdgcn_readlane(mine, Lt);
+      int gt, eq;
+      T = rank_small(lane < inb ? sbuf[lane] : 0u, inb, lane, lowT, sh, need_b, gt, eq);
+      need = need_b - gt;
+      eqT = eq;
       return true;
     }
     keys_minmax(key, lowT, highT, kmin, kmax);  // next level: the bin's own range
@@ -707,7 +580,7 @@ __device__ bool rank_keys(const uint32_t (&key)[EPT], int lane, uint32_t kmin, u
 // maxcnt the wave's largest cnt). The histogram levels of rank_keys over
 // the candidates; same outputs as rank_keys.
 __device__ void rank_segs(const uint32_t *seg, int cnt, int maxcnt, int lane, uint32_t kmin, uint32_t kmax, int c,
-                          uint32_t *hist, uint32_t *sbuf, uint32_t &T, int &need, int &eqT) {
+                          uint32_t *hist, uint32_t *sbuf, uint32_t &T, int &need, int &eqT, int stride = 1) {
   int above = 0;
 #pragma unroll 1
   for (;;) {
@@ -716,8 +589,8 @@ __device__ void rank_segs(const uint32_t *seg, int cnt, int maxcnt, int lane, ui
     *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
     wave_sync();
     for (int r = 0; r < maxcnt; ++r) {
-      const uint32_t x = r < cnt ? seg[r] : 0u;  // key 0: never inside the range
-      const bool in = x >= kmin && x <= kmax;
+      const uint32_t x = r < cnt ? seg[r * stride] : 0u;
+      const bool in = r < cnt && x >= kmin && x <= kmax;
       atomicAdd(&hist[in ? (x - kmin) >> sh : 256u + lane], 1u);
     }
     wave_sync();
@@ -761,32 +634,24 @@ __device__ void rank_segs(const uint32_t *seg, int cnt, int maxcnt, int lane, ui
     if (inb <= 64) {
       int m = 0;
       for (int r = 0; r < maxcnt; ++r) {
-        const uint32_t x = r < cnt ? seg[r] : 0u;
-        const bool in = x >= lowT && static_cast<uint64_t>(x) < highT;
+        const uint32_t x = r < cnt ? seg[r * stride] : 0u;
+        const bool in = r < cnt && x >= lowT && static_cast<uint64_t>(x) < highT;
         const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
         sbuf[in ? m + lanes_below(bal) : 64 + lane] = x;
         m += __popcll(bal);
       }
       wave_sync();
-      const uint32_t mine = lane < inb ? sbuf[lane] : 0u;
-      int gt = 0, eq = 0;
-      for (int jj = 0; jj < inb; ++jj) {
-        const uint32_t x = __builtin_amdgcn_readlane(mine, jj);
-        gt += x > mine;
-        eq += x == mine;
-      }
-      const bool isT = lane < inb && gt < need_b && need_b <= gt + eq;
-      const int Lt = __builtin_ctzll(__builtin_amdgcn_ballot_w64(isT));
-      need = need_b - __builtin_amdgcn_readlane(gt, Lt);
-      eqT = __builtin_amdgcn_readlane(eq, Lt);
-      T = __builtin_amdgcn_readlane(mine, Lt);
+      int gt, eq;
+      T = rank_small(lane < inb ? sbuf[lane] : 0u, inb, lane, lowT, sh, need_b, gt, eq);
+      need = need_b - gt;
+      eqT = eq;
       return;
     }
     // next level: the bin's own key range
     uint32_t mn = 0xffffffffu, mx = 0u;
     for (int r = 0; r < maxcnt; ++r) {
-      const uint32_t x = r < cnt ? seg[r] : 0u;
-      const bool in = x >= lowT && static_cast<uint64_t>(x) < highT;
+      const uint32_t x = r < cnt ? seg[r * stride] : 0u;
+      const bool in = r < cnt && x >= lowT && static_cast<uint64_t>(x) < highT;
       mn = in && x < mn ? x : mn;
       mx = in && x > mx ? x : mx;
     }
@@ -1178,6 +1043,500 @@ __global__ __launch_bounds__(256) void service_kernel(const SelectParams p) {
   if (i == 0 && p.gate_out) *p.gate_out = service_gate(p);
 }
 
+// ============================================================ register rows
+// Kernels for rows of at most 4096 key blocks with the row in registers in
+// the lane order of the canonical wave sum: lane j holds element k = j + 64 m
+// in slot m < EPT. The row is padded to 64 EPT elements: loads past its end
+// read +0.0 through the buffer range check, so a padding element has score
+// and risk +0 and contributes +0.0 to every sum (which leaves a float64 sum
+// of non-negative terms bit-identical). In the selection a padding element
+// has the smallest key of its row (priority +0, or key 0 on the general
+// paths) and a larger index than every real element, so with ties going to
+// the lower index it is never among the top c <= K: the per-element code
+// needs no bounds masks.
+//
+// Fast path: a row whose scores are finite and non-negative (raw bits below
+// 0x7f800000: no NaN, infinity, negative value or -0.0), in a head whose
+// innovations are finite, with a finite risk total and a finite scale. Its
+// risks, conservative arrivals and priorities are then finite and
+// non-negative, so clean_score is the identity, clamp01 is a minimum with 1
+// and the order key of a priority is its bits with the sign bit set; the
+// arithmetic and its roundings are the general path's.
+constexpr uint32_t kFinite = 0x7f800000u;  // raw bits of +inf
+
+// The lane index through an empty asm: per-element indices and masks made
+// from it are recomputed in the loop that uses them instead of being hoisted
+// out of the row loop and held (64-bit masks for every slot would spill).
+__device__ __forceinline__ int opaque_lane(int lane) {
+  asm volatile("" : "+v"(lane));
+  return lane;
+}
+
+// x[m] = src[lane + 64 m] for lane + 64 m < n, +0.0 past n, through buffer
+// resources rebased every 16 slots (every offset is 4 lane plus an immediate).
+template <int EPT>
+__device__ __forceinline__ void load_slots(float (&x)[EPT], const float *src, int n, int lane) {
+#pragma unroll
+  for (int g = 0; g < (EPT + 15) / 16; ++g) {
+    const int left = n - 1024 * g;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(src + (left > 0 ? 1024 * g : 0)), 0, left > 0 ? 4 * left : 0, 0x00020000);
+#pragma unroll
+    for (int m = 16 * g; m < EPT && m < 16 * g + 16; ++m)
+      x[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 4 * lane + 256 * (m - 16 * g), 0, 0));
+  }
+}
+
+// Arrival: one workgroup per (32-row chunk, head), kRowWaves row waves; each
+// wave takes rows w, w + kRowWaves, ... of the chunk. Per row: capacity, risk
+// total, conservative arrival, pair arrivals (to the wave's LDS row, 32 EPT
+// wide so the padding's pairs land in its tail) and their row sum; then the
+// chunk's float64 column partials in row order, as arrival_kernel. Also
+// records per row whether the select pass may take the fast path (flags).
+template <int EPT, int kRowWaves>
+__global__ __launch_bounds__(64 * kRowWaves) __attribute__((amdgpu_waves_per_eu(EPT <= 33 ? 4 : 2)))
+void arrival_rows_kernel(const SelectParams p) {
+  extern __shared__ __attribute__((aligned(16))) float alds[];
+  constexpr int kThreads = 64 * kRowWaves;
+  constexpr int kStride = 32 * EPT;  // LDS row of pair arrivals
+  constexpr int kPairs = (kStride + kThreads - 1) / kThreads;  // column partials per thread
+  const int P = static_cast<int>(p.P), K = static_cast<int>(p.K);
+  const int64_t chunk = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t q0 = chunk * kChunk;
+  const int nrows = static_cast<int>(p.Q - q0 < kChunk ? p.Q - q0 : kChunk);
+  const bool even = (lane & 1) == 0;
+  // the head's innovations (0 past the pairs), read per element as pin[(lane >> 1) + 32 m],
+  // and whether all are finite
+  float *pin = alds + kRowWaves * kStride;
+  bool bad = false;
+  for (int i = tid; i < kStride; i += kThreads) {
+    const float v = i < P ? p.innovation[bh * P + i] : 0.f;
+    pin[i] = v;
+    bad |= !(v <= kFltMax);
+  }
+  const bool head_fast = !__syncthreads_or(bad);
+  double part[kPairs];
+#pragma unroll
+  for (int i = 0; i < kPairs; ++i) part[i] = 0.0;
+  float *ap_row = alds + w * kStride;
+  const float *pin_l = pin + (lane >> 1);
+
+  float x[EPT];
+  for (int r0 = 0; r0 < nrows; r0 += kRowWaves) {
+    if (r0 + w < nrows) {
+      const int64_t row = bh * p.Q + q0 + r0 + w;
+      const float *srow = p.score + row * p.K;
+      load_slots(x, srow, K, lane);
+      int cap;
+      if (p.row_cap) {
+        cap = p.row_cap[row];
+      } else {
+        cap = p.topk < 1 ? 1 : p.topk;
+        cap = cap > K ? K : cap;
+        if (p.force_last && cap < K) {
+          const uint32_t last = order_key(srow[K - 1]);
+          const int ln = opaque_lane(lane);
+          int beat = 0;
+#pragma unroll
+          for (int m = 0; m < EPT; ++m) {
+            const int k = ln + 64 * m;
+            const uint32_t kk = order_key(x[m]);
+            beat += k < K && ((kk > last) || (kk == last && k < K - 1));
+          }
+          cap += wave_sum_int(beat) >= cap ? 1 : 0;
+        }
+      }
+      uint32_t hi = 0u;
+#pragma unroll
+      for (int m = 0; m < EPT; ++m) hi = max(hi, __float_as_uint(x[m]));
+      const bool clean = head_fast && __builtin_amdgcn_ballot_w64(hi >= kFinite) == 0;
+      // risks (in place) and their canonical sum
+      double acc = 0.0;
+      // (the innovation reads are fenced in groups of four slots, so that few
+      // of them hold registers at a time)
+      if (clean) {
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) {
+          x[m] = x[m] * pin_l[32 * m];
+          acc = acc + static_cast<double>(x[m]);
+          if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) {
+          x[m] = clean_score(x[m]) * pin_l[32 * m];
+          acc = acc + static_cast<double>(x[m]);
+          if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      const double tot = wave_butterfly(acc);
+      const float total = static_cast<float>(tot);
+      const float scale = static_cast<float>(cap) / floor_tiny(total);
+      const bool live = total > 0.f;
+      // every risk finite (a sum of finite non-negative floats stays far below the float64 limit)
+      const bool fast = clean && tot <= 1.0e300 && scale <= kFltMax;
+      double racc = 0.0;
+      if (fast && !(K & 1)) {
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) {
+          const float A = live ? fminf(x[m] * scale, 1.0f) : 0.f;
+          const float ap = (A + dpp<kQuadXor1>(A)) * 0.5f;  // both lanes of a pair form its sum (addition commutes)
+          racc = racc + static_cast<double>(even ? ap : 0.f);
+          x[m] = ap;
+        }
+      } else {
+        const int ln = opaque_lane(lane);
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) {
+          const int k = ln + 64 * m;
+          const float A = live && k < K ? (fast ? fminf(x[m] * scale, 1.0f) : clamp01(x[m] * scale)) : 0.f;
+          const float s2 = A + dpp<kQuadXor1>(A);
+          const float ap = k == K - 1 ? s2 : s2 * 0.5f;  // an odd tail pairs with itself: (A + 0) / 1
+          racc = racc + static_cast<double>(even ? ap : 0.f);
+          x[m] = ap;
+        }
+      }
+      if (even) {
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) ap_row[(lane >> 1) + 32 * m] = x[m];
+      }
+      const float rowpair = static_cast<float>(wave_butterfly(racc));
+      if (lane == 0) {
+        p.total[row] = total;
+        p.rowpair[row] = rowpair;
+        p.cap[row] = cap;
+        p.flags[row] = fast ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    const int rows_here = nrows - r0 < kRowWaves ? nrows - r0 : kRowWaves;
+    int t = tid;
+    asm volatile("" : "+v"(t));  // addresses made here, not held across the row loop
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+      const int pp = t + kThreads * i;
+      if (pp < P)
+        for (int rr = 0; rr < rows_here; ++rr) part[i] = part[i] + static_cast<double>(alds[rr * kStride + pp]);
+    }
+    __syncthreads();
+  }
+  double *out = p.part + (bh * p.nchunks + chunk) * p.P;
+#pragma unroll
+  for (int i = 0; i < kPairs; ++i) {
+    const int pp = tid + kThreads * i;
+    if (pp < P) out[pp] = part[i];
+  }
+}
+
+// Candidate keys staged per lane by the select pass (kSeg or more: the row is
+// ranked on its registers instead). Lane l's r-th candidate sits at
+// cand[64 (r & 15) + l].
+constexpr int kSeg = 16;
+// per wave: histogram (256 bins + 64 per-lane trash bins), 64 gathered keys
+// (+ 64 trash slots), candidate segments (64 kSeg words)
+constexpr int kRowWaveWords = 320 + 128 + 64 * kSeg;
+
+// The threshold of the keys of a padded row (64 EPT keys, 0 the smallest
+// any element can have, held by the padding): keys > T are kept, keys == T
+// in index order up to need (eqT of them). A histogram of a sample (lanes 4i
+// of the even slots; 256 bins over the sampled keys' range above 0)
+// brackets the c-th largest key at its sample rank c S / n -+ 3 sigma + 1;
+// keys above the bracket are kept, the bracket's keys are staged per lane
+// and ranked exactly (rank_segs). When fewer than c keys exceed 0 the
+// threshold is 0, its ties going in index order. When the bracket misses,
+// or a lane holds kSeg or more candidates, the threshold is found by
+// bisection over the key bits.
+template <int EPT>
+__device__ __forceinline__ void rows_threshold(const uint32_t (&key)[EPT], int lane, int c, uint32_t *hist,
+                                               uint32_t *sbuf, uint32_t *cand, uint32_t &T, int &need, int &eqT) {
+  constexpr int n = 64 * EPT;
+  constexpr int S = 16 * ((EPT + 1) / 2);  // samples
+  const bool sampler = (lane & 3) == 0;
+  uint32_t smin = 0xffffffffu, smax = 0u;  // smin: over sampled keys above 0, less one
+#pragma unroll
+  for (int m = 0; m < EPT; m += 2) {
+    smin = min(smin, sampler ? key[m] - 1u : 0xffffffffu);
+    smax = max(smax, sampler ? key[m] : 0u);
+  }
+#pragma unroll
+  for (int o = 32; o >= 4; o >>= 1) {
+    smin = min(smin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(smin), o)));
+    smax = max(smax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(smax), o)));
+  }
+  smin = __builtin_amdgcn_readfirstlane(smin) + 1u;  // 0 when no sampled key exceeds 0
+  smax = __builtin_amdgcn_readfirstlane(smax);
+  uint32_t hm1 = 0xffffffffu, lo = 1u;  // keys > hm1 kept outright; candidates in [lo, hm1]
+  const int rs = static_cast<int>(static_cast<int64_t>(c) * S / n);
+  const int mg = sample_margin(S, c, n);
+  if (smin != 0u && smax > smin) {
+    const uint32_t range = smax - smin;
+    const int sh = 32 - __clz(range) > 8 ? 32 - __clz(range) - 8 : 0;
+    *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
+    wave_sync();
+    if (sampler) {
+#pragma unroll
+      for (int m = 0; m < EPT; m += 2) atomicAdd(&hist[key[m] ? (key[m] - smin) >> sh : 256u + lane], 1u);
+    }
+    wave_sync();
+    u32x4 h;
+    const int suf = hist_suffix(hist, lane, h);
+    const int spos = __builtin_amdgcn_readfirstlane(suf);  // sampled keys above 0
+    if (rs - mg >= 1 && rs - mg <= spos) {
+      const int b = rank_bin(h, suf, lane, rs - mg);
+      if (b < 255) hm1 = smin + ((static_cast<uint32_t>(b) + 1u) << sh) - 1u;
+    }
+    if (rs + mg <= spos) lo = smin + (static_cast<uint32_t>(rank_bin(h, suf, lane, rs + mg)) << sh);
+    if (lo > hm1) lo = 1u;
+  }
+  // candidates [lo, hm1] into this lane's segment (each key is written at
+  // the segment's end, which advances only past a candidate); keys above hm1 counted
+  const uint32_t span = hm1 - lo;
+  uint32_t *seg = cand + lane;
+  int cnt = 0, above = 0;
+#pragma unroll
+  for (int m = 0; m < EPT; ++m) {
+    const uint32_t x = key[m];
+    above += __popcll(__builtin_amdgcn_ballot_w64(x > hm1));
+    seg[64 * (cnt & (kSeg - 1))] = x;
+    cnt += x - lo <= span ? 1 : 0;  // keys below lo (0 among them) wrap above span
+  }
+  above = __builtin_amdgcn_readfirstlane(above);
+  int tot = cnt, maxcnt = cnt;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    tot += __shfl_xor(tot, o);
+    maxcnt = max(maxcnt, __shfl_xor(maxcnt, o));
+  }
+  tot = __builtin_amdgcn_readfirstlane(tot);
+  maxcnt = __builtin_amdgcn_readfirstlane(maxcnt);
+  wave_sync();
+  // a lane with kSeg candidates has overwritten its first one with the next key
+  if (above < c && above + tot >= c && maxcnt < kSeg) {
+    rank_segs(seg, cnt, maxcnt, lane, lo, hm1, c - above, hist, sbuf, T, need, eqT, 64);
+    return;
+  }
+  if (above + tot < c && lo == 1u) {  // every key above 0 is kept; the rest of the c are 0 keys
+    T = 0u;
+    need = c - above - tot;
+    eqT = n - above - tot;
+    return;
+  }
+  // the bracket missed, or a lane's candidates overflowed: the c-th largest
+  // key by bisection over its bits (the largest t with at least c keys >= t),
+  // exact for any distribution and holding no more registers than the keys
+  uint32_t pre = 0u;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t t = pre | (1u << b);
+    int ge = 0;
+#pragma unroll
+    for (int m = 0; m < EPT; ++m) ge += __popcll(__builtin_amdgcn_ballot_w64(key[m] >= t));
+    if (ge >= c) pre = t;
+  }
+  int gt = 0, eq = 0;
+#pragma unroll
+  for (int m = 0; m < EPT; ++m) {
+    gt += __popcll(__builtin_amdgcn_ballot_w64(key[m] > pre));
+    eq += __popcll(__builtin_amdgcn_ballot_w64(key[m] == pre));
+  }
+  T = pre;
+  need = c - gt;
+  eqT = eq;
+}
+
+// Select: one wave per row, rows_per_wave consecutive rows per wave, the
+// workgroup's rows in one head. Keys in registers in the arrival's lane
+// order (kPrefetch: the next row's scores load while this row is ranked);
+// on the fast paths a key is the raw bits of the non-negative priority or
+// score, otherwise its order key (the padding's key is 0 either way). VASC:
+// the (innovation, admitted debt) table of the head and the pair counts live
+// in LDS. Index lists are written in ascending order straight from the
+// ballots: every lane stores, the unselected ones past the row's buffer
+// range, which drops them.
+template <bool kVasc, int EPT, bool kPrefetch>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EPT <= 33 ? 4 : 1)))
+void select_rows_kernel(const SelectParams p, int rows_per_wave) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  const int tid = threadIdx.x, lane0 = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int K = static_cast<int>(p.K), P = static_cast<int>(p.P);
+  uint32_t *hist = lds + w * kRowWaveWords;
+  uint32_t *sbuf = hist + 320;
+  uint32_t *cand = sbuf + 128;
+  uint32_t *pair_cnt = lds + kWaves * kRowWaveWords;  // 32 EPT words, one per pair (VASC)
+  float2 *ia_s = reinterpret_cast<float2 *>(pair_cnt + 32 * EPT);  // 32 EPT entries (VASC), 0 past P
+  const int64_t bh = blockIdx.y;
+  int gate = 0;
+  bool ia_fast = true;
+  if (kVasc) {
+    bool bad = false;
+    for (int i = tid; i < 32 * EPT; i += 256) {
+      const float2 v = i < P ? p.ia[bh * P + i] : float2{0.f, 0.f};
+      ia_s[i] = v;
+      bad |= !(v.y <= kFltMax);
+      pair_cnt[i] = 0u;
+    }
+    ia_fast = !__syncthreads_or(bad);
+    gate = service_gate(p);
+  }
+
+  float x[EPT], nxt[EPT];
+  const int64_t q_first = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * rows_per_wave;
+  if (kPrefetch && q_first < p.Q) load_slots(nxt, p.score + (bh * p.Q + q_first) * p.K, K, lane0);
+  for (int rr = 0; rr < rows_per_wave; ++rr) {
+    const int64_t q = q_first + rr;
+    if (q >= p.Q) break;
+    // lane-derived values and masks are recomputed per row, not held across rows
+    const int lane = opaque_lane(lane0);
+    const int64_t row = bh * p.Q + q;
+    const float *srow = p.score + row * p.K;
+    if (kPrefetch) {
+#pragma unroll
+      for (int m = 0; m < EPT; ++m) x[m] = nxt[m];
+      if (rr + 1 < rows_per_wave && q + 1 < p.Q) load_slots(nxt, srow + p.K, K, lane);
+    } else {
+      load_slots(x, srow, K, lane);
+    }
+    // ---- keys
+    uint32_t key[EPT];
+    int c;
+    bool exact_keys;  // order keys, real elements masked against the row end
+    if (kVasc) {
+      const int cap = p.cap[row];
+      c = cap < p.max_capacity ? cap : p.max_capacity;
+      const float total = p.total[row];
+      const float scale = static_cast<float>(cap) / floor_tiny(total);
+      const bool live = total > 0.f;
+      // with the gate on and K odd, the padding element K shares pair P - 1's admitted debt,
+      // so its fast-path key would not be the row's smallest: the masked path handles it
+      exact_keys = !(p.flags[row] && (gate == 0 || (ia_fast && (K & 1) == 0)));
+      const float2 *ia_l = ia_s + (lane >> 1);
+      // (the table reads are fenced in groups of four slots, so that few of
+      // them hold registers at a time)
+      if (!exact_keys) {
+        if (!live) {
+#pragma unroll
+          for (int m = 0; m < EPT; ++m) {
+            key[m] = gate ? __float_as_uint(ia_l[32 * m].y) : 0u;
+            if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+          }
+        } else if (gate) {
+#pragma unroll
+          for (int m = 0; m < EPT; ++m) {
+            const float2 ia = ia_l[32 * m];
+            key[m] = __float_as_uint(fminf((x[m] * ia.x) * scale, 1.0f) + ia.y);
+            if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+#pragma unroll
+          for (int m = 0; m < EPT; ++m) {
+            key[m] = __float_as_uint(fminf((x[m] * ia_l[32 * m].x) * scale, 1.0f));
+            if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      } else {
+        const int ln = opaque_lane(lane);
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) {
+          const int k = ln + 64 * m;
+          const float2 ia = ia_l[32 * m];
+          const float A = live ? clamp01((clean_score(x[m]) * ia.x) * scale) : 0.f;
+          key[m] = k < K ? order_key(gate ? A + ia.y : A) : 0u;
+          if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      if (p.priority_out) {
+        const int ln = opaque_lane(lane);
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) {
+          const int k = ln + 64 * m;
+          if (k < K) p.priority_out[row * p.K + k] = __uint_as_float(exact_keys ? key[m] & 0x7fffffffu : key[m]);
+        }
+      }
+    } else {
+      c = p.row_cap ? p.row_cap[row] : p.topk;
+      c = c < 1 ? 1 : c;
+      const int lim = p.max_capacity >= K ? K : p.max_capacity;
+      if (p.row_cap) c = c < lim ? c : lim;
+      c = c > K ? K : c;
+      uint32_t hi = 0u;
+#pragma unroll
+      for (int m = 0; m < EPT; ++m) hi = max(hi, __float_as_uint(x[m]));
+      // non-negative, non-NaN scores (+inf included) order as their bits
+      exact_keys = __builtin_amdgcn_ballot_w64(hi > kFinite) != 0;
+      if (!exact_keys) {
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) key[m] = __float_as_uint(x[m]);
+      } else {
+        const int ln = opaque_lane(lane);
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) key[m] = ln + 64 * m < K ? order_key(x[m]) : 0u;
+      }
+    }
+    c = c < 0 ? 0 : (c > K ? K : c);
+    c = __builtin_amdgcn_readfirstlane(c);
+
+    // ---- threshold: keys > T kept, keys == T kept in index order up to need
+    uint32_t T = 0xffffffffu;  // c == 0: nothing is kept (no key reaches T with need 0)
+    int need = 0, eqT = 1;
+    if (c > 0) rows_threshold(key, lane, c, hist, sbuf, cand, T, need, eqT);
+    const bool split = need < eqT;
+
+    // ---- ascending compaction straight to the index row and pair counts
+    const __amdgpu_buffer_rsrc_t irs =
+        __builtin_amdgcn_make_buffer_rsrc(p.index_out + row * p.width, 0, static_cast<int>(4 * p.width), 0x00020000);
+    uint32_t *cnt_l = pair_cnt + (lane >> 1);
+    int base = 0, run_eq = 0;
+#pragma unroll
+    for (int m = 0; m < EPT; ++m) {
+      const uint32_t xk = key[m];
+      bool sel;
+      if (!split) {
+        sel = xk >= T;
+      } else {
+        const bool eq = xk == T;
+        const uint64_t beq = __builtin_amdgcn_ballot_w64(eq);
+        sel = xk > T || (eq && run_eq + lanes_below(beq) < need);
+        run_eq += __popcll(beq);
+      }
+      const uint64_t bm = __builtin_amdgcn_ballot_w64(sel);
+      // unselected lanes store past the buffer range (dropped)
+      __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(lane + 64 * m), irs,
+                                            sel ? 4 * (base + lanes_below(bm)) : 0x7ffffff0, 0, 0);
+      if (kVasc) atomicAdd(&cnt_l[32 * m], sel ? 1u : 0u);
+      base += __popcll(bm);
+    }
+    if (p.mask_out) {
+      uint8_t *mrow = p.mask_out + row * p.K;
+      const int ln = opaque_lane(lane);
+      run_eq = 0;
+#pragma unroll
+      for (int m = 0; m < EPT; ++m) {
+        const int k = ln + 64 * m;
+        const uint32_t xk = key[m];
+        bool sel = xk >= T;
+        if (split) {
+          const bool eq = xk == T;
+          const uint64_t beq = __builtin_amdgcn_ballot_w64(eq);
+          sel = xk > T || (eq && run_eq + lanes_below(beq) < need);
+          run_eq += __popcll(beq);
+        }
+        if (k < K) mrow[k] = sel ? 1 : 0;
+      }
+    }
+    int32_t *irow = p.index_out + row * p.width;
+    for (int i = lane; i < p.sink && base + i < p.width; i += 64) irow[base + i] = static_cast<int32_t>(p.K + i);
+    for (int64_t e = base + p.sink + lane; e < p.width; e += 64) irow[e] = -1;  // the rest of the row defined
+    if (lane == 0) p.count_out[row] = base + p.sink;
+  }
+  if (kVasc) {
+    __syncthreads();
+    for (int64_t i = tid; i < p.P; i += 256)
+      if (pair_cnt[i]) atomicAdd(&p.counts[bh * p.P + i], static_cast<int32_t>(pair_cnt[i]));
+  }
+}
+
 __global__ void settle_terminal_kernel(const float *debt_in, const float *pending, const float *service, int64_t n,
                                        float *out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -1187,7 +1546,7 @@ __global__ void settle_terminal_kernel(const float *debt_in, const float *pendin
 }
 
 struct Workspace {
-  size_t total, rowpair, cap, adm, ia, part, gate_part, counts, bytes;
+  size_t total, rowpair, cap, adm, ia, part, gate_part, counts, flags, bytes;
 };
 
 Workspace layout(int64_t B, int64_t H, int64_t Q, int64_t K) {
@@ -1202,6 +1561,7 @@ Workspace layout(int64_t B, int64_t H, int64_t Q, int64_t K) {
   w.part = off;      off += align256(BH * static_cast<size_t>(cdiv(Q, kChunk)) * P * 8);
   w.gate_part = off; off += align256(BH * 3 * 8);
   w.counts = off;    off += align256(BH * P * 4);
+  w.flags = off;     off += align256(BH * Q * 4);
   w.bytes = off;
   return w;
 }
@@ -1250,7 +1610,43 @@ int launch_select_mode(const SelectParams &p, hipStream_t s) {
   return launch_select_cfg<kVasc, 128>(p, s);
 }
 
+// Register-row select for K <= 4096 (not with protected blocks or a forced
+// last block, which the staged kernel handles).
+template <bool kVasc, int EPT>
+int launch_select_rows_cfg(const SelectParams &p, hipStream_t s) {
+  const int64_t rows = p.BH * p.Q;
+  const int rpw = static_cast<int>(rows >= 4 * 8192 ? 4 : (rows >= 2 * 8192 ? 2 : 1));
+  constexpr bool kPrefetch = false;
+  // per wave rank buffers; VASC: pair counts (32 EPT words) and the (innovation, debt) table (32 EPT float2)
+  const size_t lds_bytes = static_cast<size_t>(kWaves) * kRowWaveWords * 4 + (kVasc ? 384 * static_cast<size_t>(EPT) : 0);
+  const void *kern = reinterpret_cast<const void *>(select_rows_kernel<kVasc, EPT, kPrefetch>);
+  int rc;
+  if ((rc = reserve_lds(kern, lds_bytes))) return rc;
+  const dim3 grid(static_cast<unsigned>(cdiv(p.Q, static_cast<int64_t>(kWaves) * rpw)), static_cast<unsigned>(p.BH));
+  hipLaunchKernelGGL((select_rows_kernel<kVasc, EPT, kPrefetch>), grid, dim3(256), lds_bytes, s, p, rpw);
+  return check_launch("vasc_select_blocks/select");
+}
+
+template <bool kVasc>
+int launch_select_rows(const SelectParams &p, hipStream_t s) {
+  const int64_t K = p.K;
+  if (K <= 256) return launch_select_rows_cfg<kVasc, 4>(p, s);
+  if (K <= 576) return launch_select_rows_cfg<kVasc, 9>(p, s);
+  if (K <= 768) return launch_select_rows_cfg<kVasc, 12>(p, s);
+  if (K <= 1088) return launch_select_rows_cfg<kVasc, 17>(p, s);
+  if (K <= 1536) return launch_select_rows_cfg<kVasc, 24>(p, s);
+  if (K <= 2112 || !kVasc) return launch_select_rows_cfg<kVasc, 33>(p, s);
+  if (K <= 3072) return launch_select_rows_cfg<kVasc, 48>(p, s);
+  return launch_select_rows_cfg<kVasc, 64>(p, s);
+}
+
+// Register rows serve VASC up to 4096 key blocks (after the register-row
+// arrival) and Top-K up to 2112; wider Top-K rows, protected blocks and a
+// forced last block take the staged kernel (measured faster for Top-K at
+// 4096 key blocks, where the register rows are load-latency bound).
 int launch_select(const SelectParams &p, bool vasc, hipStream_t s) {
+  if (!p.protected_mask && !p.force_last && p.K <= (vasc ? 64 * 64 : 33 * 64))
+    return vasc ? launch_select_rows<true>(p, s) : launch_select_rows<false>(p, s);
   return vasc ? launch_select_mode<true>(p, s) : launch_select_mode<false>(p, s);
 }
 
@@ -1259,26 +1655,27 @@ int launch_select(const SelectParams &p, bool vasc, hipStream_t s) {
 // of up to 16 elements (K <= 1024, grids of ~150 chunks at C2) take sixteen.
 // Wider rows keep four row waves (two waves per SIMD, register bound).
 template <int EPT>
-int launch_arrival_reg_cfg(const SelectParams &p, hipStream_t s) {
-  constexpr int kRowWaves = EPT <= 16 ? 16 : (EPT <= 36 ? 8 : 4);
-  const size_t lds_bytes = static_cast<size_t>((1 + kRowWaves) * p.P) * 4;  // innovation + pair arrivals per row wave
-  const void *kern = reinterpret_cast<const void *>(arrival_reg_kernel<EPT, kRowWaves>);
+int launch_arrival_rows_cfg(const SelectParams &p, hipStream_t s) {
+  constexpr int kRowWaves = EPT <= 17 ? 16 : (EPT <= 33 ? 8 : 4);
+  // pair arrivals per row wave, then the innovation table
+  const size_t lds_bytes = static_cast<size_t>(kRowWaves + 1) * 32 * EPT * 4;
+  const void *kern = reinterpret_cast<const void *>(arrival_rows_kernel<EPT, kRowWaves>);
   int rc;
   if ((rc = reserve_lds(kern, lds_bytes))) return rc;
-  hipLaunchKernelGGL((arrival_reg_kernel<EPT, kRowWaves>),
+  hipLaunchKernelGGL((arrival_rows_kernel<EPT, kRowWaves>),
                      dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)), dim3(64 * kRowWaves), lds_bytes,
                      s, p);
   return VASC_OK;
 }
-int launch_arrival_reg(const SelectParams &p, hipStream_t s) {
+int launch_arrival_rows(const SelectParams &p, hipStream_t s) {
   const int64_t K = p.K;
-  if (K <= 512) return launch_arrival_reg_cfg<8>(p, s);
-  if (K <= 1024) return launch_arrival_reg_cfg<16>(p, s);
-  if (K <= 1536) return launch_arrival_reg_cfg<24>(p, s);
-  if (K <= 2048) return launch_arrival_reg_cfg<32>(p, s);
-  if (K <= 2304) return launch_arrival_reg_cfg<36>(p, s);
-  if (K <= 3072) return launch_arrival_reg_cfg<48>(p, s);
-  return launch_arrival_reg_cfg<64>(p, s);
+  if (K <= 256) return launch_arrival_rows_cfg<4>(p, s);
+  if (K <= 576) return launch_arrival_rows_cfg<9>(p, s);
+  if (K <= 1088) return launch_arrival_rows_cfg<17>(p, s);
+  if (K <= 1536) return launch_arrival_rows_cfg<24>(p, s);
+  if (K <= 2112) return launch_arrival_rows_cfg<33>(p, s);
+  if (K <= 3072) return launch_arrival_rows_cfg<48>(p, s);
+  return launch_arrival_rows_cfg<64>(p, s);
 }
 
 int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
@@ -1286,7 +1683,7 @@ int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
   int rc;
   if (vasc) {
     if (p.K <= 64 * 64) {
-      if ((rc = launch_arrival_reg(p, s))) return rc;
+      if ((rc = launch_arrival_rows(p, s))) return rc;
     } else {
       // As many waves per chunk (16, 8 or 4) as keep the row buffers within
       // 64 KB; the column partials then need P <= 16 * (64 * waves).
@@ -1423,6 +1820,7 @@ int select_blocks_impl(const float *score, const float *innovation, int64_t B, i
   p.gate_part = vasc ? reinterpret_cast<double *>(wsb + ws.gate_part) : nullptr;
   p.nchunks = cdiv(Q, kChunk);
   p.counts = vasc ? reinterpret_cast<int32_t *>(wsb + ws.counts) : nullptr;
+  p.flags = vasc ? reinterpret_cast<int32_t *>(wsb + ws.flags) : nullptr;
 
   return launch_rows(p, vasc, reinterpret_cast<hipStream_t>(stream));
 }
