@@ -405,6 +405,41 @@ int vasc_pack_qkv(const uint16_t *q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                   uint16_t *v_out, void *stream);
 
 /*
+ * Kernel 5a + 1a + 3 fused for a global layer that pools by block means:
+ * the layout of vasc_pack_qkv (same inputs, same q_patch / q_special /
+ * k_out, bit for bit) together with
+ *   vt          V of the [patch; special] order as vasc_pack_v's MFMA tiles
+ *               [B,H,ceil(N*P/64),d,64] (V is never written in token rows);
+ *   pooled_q    [B,H,ceil(Np/128),d], pooled_k / pooled_v [B,H,ceil(Np/64),d]
+ *               (Np = N*(P-S)): bf16 block means of the packed patch q / k
+ *               and of the patch v, tail blocks over their real tokens
+ *               (predict_attention, attention.py:31-104, on q_patch and the
+ *               patch keys; _mean_pool_contiguous_value_blocks,
+ *               sparse_wrapper.py:2839-2861); each may be NULL;
+ *   innovation  [B,H,ceil(ceil(Np/64)/2)] float32 pair innovation of the
+ *               pooled V blocks (sparse_wrapper.py:3733-3740), or NULL.
+ * No single reference function does this: it replaces the layout of
+ * attention.py:8351-8469, the pooling of attention.py:31-104 and the value
+ * pooling of sparse_wrapper.py:2839-2861 and 3733-3740 in one pass, so the
+ * packed q, k and the V tiles are read again only by the attention. Pooled
+ * sums are float32 in a fixed order (per thread, then the 8 row groups of a
+ * wave, then the four waves), within one bf16 rounding of the exact mean.
+ * Requires S < P. Built variant: d == 64.
+ */
+int vasc_pack_global(const uint16_t *q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                     const uint16_t *k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                     const uint16_t *v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                     int64_t B, int64_t H, int64_t N, int64_t P, int64_t S,
+                     int64_t d, const void *q_norm_w, const void *q_norm_b,
+                     float q_eps, int32_t q_norm, const void *k_norm_w,
+                     const void *k_norm_b, float k_eps, int32_t k_norm,
+                     const int32_t *pos, int64_t pos_sb, int64_t pos_st,
+                     const float *rope_cos, const float *rope_sin, int64_t rope_n,
+                     uint16_t *q_patch, uint16_t *q_special, uint16_t *k_out,
+                     uint16_t *vt, uint16_t *pooled_q, uint16_t *pooled_k,
+                     uint16_t *pooled_v, float *innovation, void *stream);
+
+/*
  * Kernel 5b: attention outputs in [patch; special] order back to the
  * frame-major token layout the output projection reads (attention.py:
  * 8992-9027 with tokens.py:102-126 and the transpose/reshape):

@@ -151,8 +151,9 @@ def _ref_pi3(model, images, lists=None):
 
 
 class _Recorder:
-    """Records, per sparse global layer, the pooled scores, the value tensor
-    and the index lists that the selection produced."""
+    """Records, per sparse global layer, the pooled scores, the values' pair
+    innovation the selection was given (or the value tensor, when the
+    caller handed the values instead) and the index lists it produced."""
 
     def __init__(self, monkeypatch):
         from vasc_amd import sparse_wrapper
@@ -161,7 +162,9 @@ class _Recorder:
 
         def record(key, value, pooled_score, *args, **kwargs):
             sel, total = original(key, value, pooled_score, *args, **kwargs)
-            self.layers.append({"prob": pooled_score.clone(), "value": value.clone(),
+            inn = kwargs.get("innovation")
+            self.layers.append({"prob": pooled_score.clone(), "value": None if value is None else value.clone(),
+                                "innovation": None if inn is None else inn.clone(),
                                 "index": sel["index"].clone(), "count": sel["count"].clone()})
             return sel, total
 
@@ -176,7 +179,10 @@ def _oracle_chain(layers, n_patch, n_total, ratios, mode, official):
     for li, rec in enumerate(layers):
         iota = None
         if mode == "vasc":
-            iota = ops.pool_qkv(v=rec["value"][..., :n_patch, :])[3].cpu().numpy()
+            inn = rec["innovation"]
+            if inn is None:
+                inn = ops.pool_qkv(v=rec["value"][..., :n_patch, :])[3]
+            iota = inn.cpu().numpy()
         final, _ = OS.layer_selection(rec["prob"].cpu().numpy(), mode=mode, sparse_ratio=ratios[li],
                                       patch_tokens=n_patch, total_tokens=n_total, official_mask=official,
                                       state=state, layer_idx=li, iota=iota)

@@ -113,6 +113,72 @@ def test_pack_without_v_and_strided_v_tiles(N, P, S, H):
         assert np.array_equal(_bits(vt_strided), _bits(ops.pack_v(full[3])))
 
 
+def _one_bf16_rounding(got, ref):
+    """Pooled means within one bf16 rounding of the float64 mean (the
+    kernel's float32 sums may round the other way)."""
+    got = got.float().cpu().numpy().astype(np.float64)
+    bad = np.abs(got - ref) > np.abs(ref) * 2.0 ** -7 + 1e-30
+    assert not bad.any(), f"{bad.sum()} pooled values off by more than one bf16 rounding"
+
+
+@pytest.mark.parametrize("N,P,S,H,B,transform", [
+    (3, 1041, 5, 2, 1, True),    # C1-like frames, norm + rotary, ragged tails
+    (2, 37, 0, 3, 2, False),     # no special tokens, two batch entries
+    (1, 131, 4, 16, 1, True),    # 16 heads, one query block, odd key-block count
+    (4, 6, 5, 1, 1, False),      # one patch token per frame
+    (2, 69, 5, 2, 1, True),      # patch tokens exactly one query block, special tail block
+    (2, 70, 5, 2, 2, False),     # 130 patch tokens: odd key blocks, 2-token tail
+    (1, 8192 + 5, 5, 1, 1, True),  # 8192 patch tokens: no tail
+])
+def test_pack_global_matches_separate_passes(N, P, S, H, B, transform):
+    """The fused layout + pooling + V tiles against the separate passes it
+    replaces: q_patch, q_special and k bit-identical to pack_qkv, the V tiles
+    bit-identical to pack_v of pack_qkv's v, the pooled means within one bf16
+    rounding of the float64 block means of the packed patch tokens (the
+    oracle's pool_blocks), the innovation bit-exact given the pooled values."""
+    from oracle import selector as OS
+    from oracle import pooling as OP
+    from vasc_amd import ops
+    from vasc_amd.aggregator import RotaryPositionEmbedding2D
+    D, T = 64, N * P
+    qkv = _bf16((B, T, 3 * H * D), N * 31 + P, 2.0).cuda().view(B, T, 3, H, D)
+    kw = {}
+    if transform:
+        g = torch.Generator().manual_seed(P)
+        qw, qb, kwt = (torch.randn(D, generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+        pos = torch.randint(0, 40, (B, T, 2), generator=g).cuda()
+        kw = dict(q_norm=(qw, qb, 1e-6), k_norm=(kwt, None, 1e-5), pos=pos,
+                  rope_tables=RotaryPositionEmbedding2D().tables(D, "cuda"))
+    sep = ops.pack_qkv(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], N, P, S, **kw)
+    qp, qs, k, vt, pq, pk, inn, pv = ops.pack_global(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], N, P, S,
+                                                     pooled_v=True, **kw)
+    assert np.array_equal(_bits(qp), _bits(sep[0]))
+    assert (qs is None) == (sep[1] is None)
+    if qs is not None:
+        assert np.array_equal(_bits(qs), _bits(sep[1]))
+    assert np.array_equal(_bits(k), _bits(sep[2]))
+    assert np.array_equal(_bits(vt), _bits(ops.pack_v(sep[3])))
+    n_patch = N * (P - S)
+    _one_bf16_rounding(pq, OP.pool_blocks(_to_np(sep[0]), 128))
+    _one_bf16_rounding(pk, OP.pool_blocks(_to_np(sep[2])[:, :, :n_patch], 64))
+    _one_bf16_rounding(pv, OP.pool_blocks(_to_np(sep[3])[:, :, :n_patch], 64))
+    expect = OS.innovation(pv.float().cpu().numpy())
+    assert inn.shape == expect.shape
+    assert np.array_equal(inn.cpu().numpy().view(np.uint32), expect.view(np.uint32))
+    # without the optional outputs the required ones do not change
+    bare = ops.pack_global(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], N, P, S, innovation=False, **kw)
+    assert bare[6] is None and bare[7] is None
+    for a, b in ((bare[0], qp), (bare[2], k), (bare[3], vt), (bare[4], pq), (bare[5], pk)):
+        assert np.array_equal(_bits(a), _bits(b))
+
+
+def test_pack_global_rejects_frames_without_patch_tokens():
+    from vasc_amd import ops
+    x = _bf16((1, 12, 3, 1, 64), 5).cuda()
+    with pytest.raises(ValueError, match="patch token"):
+        ops.pack_global(x[:, :, 0], x[:, :, 1], x[:, :, 2], 2, 6, 6)
+
+
 @pytest.mark.parametrize("N,P,S", [(3, 1041, 5), (2, 50, 0), (2, 7, 7)])
 def test_restore_bit_exact(N, P, S):
     from vasc_amd import ops
@@ -266,8 +332,9 @@ def test_global_layer_vasc_chain_matches_oracle(backbone, monkeypatch):
     output matches the oracle layer (norms, rotary, reorder, attention over
     those lists, special queries over every key, restore) through proj."""
     import os
+    from oracle import pooling as OP
     from oracle import selector as OS
-    from vasc_amd import launcher, ops, sparse_wrapper
+    from vasc_amd import launcher, sparse_wrapper
     from vasc_amd.aggregator import Attention, RotaryPositionEmbedding2D
     from vasc_amd.attention import adaptive_sparse_attention_forward
 
@@ -276,8 +343,9 @@ def test_global_layer_vasc_chain_matches_oracle(backbone, monkeypatch):
 
     def record(key, value, pooled_score, *args, **kwargs):
         sel, total = original(key, value, pooled_score, *args, **kwargs)
-        recorded.append({"prob": pooled_score.clone(), "value": value.clone(), "index": sel["index"].clone(),
-                         "count": sel["count"].clone()})
+        assert value is None, "the fused layout hands over the V tiles, not the values"
+        recorded.append({"prob": pooled_score.clone(), "innovation": kwargs["innovation"].clone(),
+                         "index": sel["index"].clone(), "count": sel["count"].clone()})
         return sel, total
 
     monkeypatch.setattr(sparse_wrapper, "_select_for_layer", record)
@@ -315,10 +383,10 @@ def test_global_layer_vasc_chain_matches_oracle(backbone, monkeypatch):
     state: dict = {}
     bf = lambda a: torch.from_numpy(a).to(torch.bfloat16).float().numpy()  # noqa: E731
     for layer, (rec, m, x, out) in enumerate(zip(recorded, mods, xs_in, outs)):
-        _, _, _, iota = ops.pool_qkv(v=rec["value"][..., :n_patch, :])
+        iota = rec["innovation"].cpu().numpy()
         final, _ = OS.layer_selection(rec["prob"].cpu().numpy(), mode="vasc", sparse_ratio=0.5, patch_tokens=n_patch,
                                       total_tokens=n_total, official_mask=official, state=state, layer_idx=layer,
-                                      iota=iota.cpu().numpy())
+                                      iota=iota)
         idx, cnt = OS.index_lists(final)
         got_i, got_c = rec["index"].cpu().numpy(), rec["count"].cpu().numpy()
         assert np.array_equal(got_c, cnt), f"layer {layer}: counts differ from the oracle"
@@ -336,6 +404,17 @@ def test_global_layer_vasc_chain_matches_oracle(backbone, monkeypatch):
                 q_norm=(m.q_norm.weight.float().cpu().numpy(), m.q_norm.bias.float().cpu().numpy(), m.q_norm.eps),
                 k_norm=(m.k_norm.weight.float().cpu().numpy(), m.k_norm.bias.float().cpu().numpy(), m.k_norm.eps),
                 pos=pos[0].cpu().numpy(), tables=(cos.cpu().numpy(), sin.cpu().numpy()))
+        # the layer's innovation against the oracle's from the oracle's packed
+        # values: their bf16 block means may differ by one rounding per
+        # element, which moves 0.5 ||l - r|| / sqrt(D) by at most half the
+        # norm of those roundings (triangle inequality), plus float32 error
+        ref_pv = OP.pool_blocks(bf(vre)[:, :, :n_patch], 64, round_bf16=True)
+        ref_iota = OS.innovation(ref_pv)
+        sp = OP.bf16_spacing(np.abs(ref_pv) * (1 + 2.0 ** -7))  # the larger gap when a mean rounds up a binade
+        if sp.shape[-2] % 2:
+            sp = np.concatenate([sp, sp[..., -1:, :]], axis=-2)
+        step = 0.5 * np.sqrt(((sp[..., 0::2, :] + sp[..., 1::2, :]) ** 2).mean(-1))
+        assert (np.abs(iota - ref_iota) <= step + 1e-6 * ref_iota + 1e-30).all(), f"layer {layer}: innovation"
         o_p = OA.block_sparse_attention(bf(qp), bf(kre), bf(vre), got_i, got_c)
         dl, dc = OA.dense_lists(1, heads, N * S, n_total)
         o_s = OA.block_sparse_attention(bf(qsp), bf(kre), bf(vre), dl, dc)

@@ -60,6 +60,9 @@ SIGNATURES: dict[str, tuple] = {
     "vasc_pack_qkv": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64,
                                 I64, I64, I64, I64, I64, I64, P, P, c_float, I32, P, P, c_float, I32,
                                 P, I64, I64, P, P, I64, P, P, P, P, P]),
+    "vasc_pack_global": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64,
+                                   I64, I64, I64, I64, I64, I64, P, P, c_float, I32, P, P, c_float, I32,
+                                   P, I64, I64, P, P, I64, P, P, P, P, P, P, P, P, P]),
     "vasc_restore_tokens": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64, I64, I64,
                                       P, P]),
     # include/vasc_runner.h

@@ -118,6 +118,22 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
     Hp, Wp, N, P = _infer_frames(pos, NP, S)
     qkv = self.qkv(x).to(torch.bfloat16).view(B, NP, 3, nh, hd)
     rope = getattr(self, "rope", None)
+    n_patch = N * (P - S)
+    vasc_mode = routing_config().mode == "vasc"
+    if pool_mode == "avg" and n_patch > 0 and fused_layout_supported(self):
+        # layout, V tiles, block means and value innovation in one pass
+        tables = rope.tables(hd, x.device) if rope is not None else None
+        q_patch, q_special, k_re, vt, pq, pk, innovation, _ = ops.pack_global(
+            qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], N, P, S, q_norm=layer_norm_args(self.q_norm),
+            k_norm=layer_norm_args(self.k_norm), pos=pos if rope is not None else None, rope_tables=tables,
+            innovation=vasc_mode)
+        attn_pooled = ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(hd))
+        tokens_out, _, sparsity = sparse_global_attention(
+            q_patch, q_special, k_re, None, attn_pooled, sparse_ratio=sparse_ratio, cdf_threshold=cdf_threshold,
+            layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch,
+            want_sparsity=aux_output_store is not None, _innovation=innovation, token_layout=(N, P, S), _vt=vt,
+            **research)
+        return _finish(self, x, tokens_out, sparsity, aux_output_store)
     if fused_layout_supported(self):
         tables = rope.tables(hd, x.device) if rope is not None else None
         q_patch, q_special, k_re, v_re = ops.pack_qkv(
@@ -130,9 +146,8 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
             q, k = rope(q, pos), rope(k, pos)
         q_patch, q_special, k_re, v_re = ops.pack_qkv(
             *(t.to(torch.bfloat16).transpose(1, 2) for t in (q, k, v)), N, P, S)
-    n_patch = N * (P - S)
     innovation = None
-    if pool_mode == "avg" and routing_config().mode == "vasc":
+    if pool_mode == "avg" and vasc_mode:
         # Q, K and V pooled in one pass: predict_attention's pooled Q/K and
         # the selector's value innovation
         pq, pk, _, innovation = ops.pool_qkv(q_patch, k_re[:, :, :n_patch], v_re[:, :, :n_patch])
@@ -143,6 +158,11 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
         q_patch, q_special, k_re, v_re, attn_pooled, sparse_ratio=sparse_ratio, cdf_threshold=cdf_threshold,
         layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch,
         want_sparsity=aux_output_store is not None, _innovation=innovation, token_layout=(N, P, S), **research)
+    return _finish(self, x, tokens_out, sparsity, aux_output_store)
+
+
+def _finish(self, x: torch.Tensor, tokens_out: torch.Tensor, sparsity, aux_output_store: dict | None):
+    """Output projection of the frame-major attention output (ATT:9028-9031)."""
     if aux_output_store is not None:
         aux_output_store["sparsity"] = sparsity
     out = self.proj(tokens_out.to(x.dtype))  # already in frame-major token order

@@ -450,27 +450,9 @@ def residual_norm(x: torch.Tensor, y: torch.Tensor, gamma: torch.Tensor | None =
     return xo, no
 
 
-def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, frames: int, tokens_per_frame: int,
-             special: int, *, q_norm=None, k_norm=None, pos: torch.Tensor | None = None,
-             rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None):
-    """Frame-major ``[B,T,H,D]`` q/k/v views -> ``(q_patch, q_special, k, v)``
-    in the global layer's ``[patch; special]`` order, ``[B,H,*,D]`` bf16.
-    ``v=None`` packs only q and k (the returned v is None).
-
-    ``q_norm`` / ``k_norm``: ``(weight or None, bias or None, eps)`` of a
-    per-head LayerNorm, or None. ``pos`` int ``[B,T,2]`` (row, column) with
-    ``rope_tables = (cos, sin)`` float32 ``[n, D/4]``: 2D rotary embedding.
-    """
-    B, T, H, D = q.shape
-    N, P, S = int(frames), int(tokens_per_frame), int(special)
-    if N * P != T or k.shape != q.shape or (v is not None and v.shape != q.shape):
-        raise ValueError(f"q/k/v must be [B,{N}*{P},H,D], got {tuple(q.shape)}, {tuple(k.shape)}, "
-                         f"{None if v is None else tuple(v.shape)}")
-    dev = q.device
-    qp = torch.empty(B, H, N * (P - S), D, device=dev, dtype=torch.bfloat16)
-    qs = torch.empty(B, H, N * S, D, device=dev, dtype=torch.bfloat16)
-    ko = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
-    vo = None if v is None else torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+def _layout_args(B: int, T: int, D: int, q_norm, k_norm, pos, rope_tables) -> tuple[list, tuple]:
+    """The norm and rotary arguments of the layout entry points:
+    ``(tensors to keep alive, (q norm x4, k norm x4, rope x6))``."""
     keep = []
 
     def norm_args(nrm, name):
@@ -508,12 +490,76 @@ def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, frames: i
         keep += [pos32, cos, sin]
         rope = (pos32.data_ptr(), pos32.stride(0) if pos32.shape[0] > 1 else 0, pos32.stride(1), cos.data_ptr(),
                 sin.data_ptr(), cos.shape[0])
-    qn, kn = norm_args(q_norm, "q_norm"), norm_args(k_norm, "k_norm")
+    return keep, (*norm_args(q_norm, "q_norm"), *norm_args(k_norm, "k_norm"), *rope)
+
+
+def pack_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, frames: int, tokens_per_frame: int,
+             special: int, *, q_norm=None, k_norm=None, pos: torch.Tensor | None = None,
+             rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None):
+    """Frame-major ``[B,T,H,D]`` q/k/v views -> ``(q_patch, q_special, k, v)``
+    in the global layer's ``[patch; special]`` order, ``[B,H,*,D]`` bf16.
+    ``v=None`` packs only q and k (the returned v is None).
+
+    ``q_norm`` / ``k_norm``: ``(weight or None, bias or None, eps)`` of a
+    per-head LayerNorm, or None. ``pos`` int ``[B,T,2]`` (row, column) with
+    ``rope_tables = (cos, sin)`` float32 ``[n, D/4]``: 2D rotary embedding.
+    """
+    B, T, H, D = q.shape
+    N, P, S = int(frames), int(tokens_per_frame), int(special)
+    if N * P != T or k.shape != q.shape or (v is not None and v.shape != q.shape):
+        raise ValueError(f"q/k/v must be [B,{N}*{P},H,D], got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{None if v is None else tuple(v.shape)}")
+    dev = q.device
+    qp = torch.empty(B, H, N * (P - S), D, device=dev, dtype=torch.bfloat16)
+    qs = torch.empty(B, H, N * S, D, device=dev, dtype=torch.bfloat16)
+    ko = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+    vo = None if v is None else torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+    keep, args = _layout_args(B, T, D, q_norm, k_norm, pos, rope_tables)
     vsrc = (None, 0, 0, 0) if v is None else _btht(v, "v")
-    _lib.call("vasc_pack_qkv", *_btht(q, "q"), *_btht(k, "k"), *vsrc, B, H, N, P, S, D,
-              qn[0], qn[1], qn[2], qn[3], kn[0], kn[1], kn[2], kn[3], *rope,
+    _lib.call("vasc_pack_qkv", *_btht(q, "q"), *_btht(k, "k"), *vsrc, B, H, N, P, S, D, *args,
               qp.data_ptr(), qs.data_ptr(), ko.data_ptr(), _ptr(vo), _stream())
+    del keep
     return qp, (qs if S else None), ko, vo
+
+
+def pack_global(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, frames: int, tokens_per_frame: int,
+                special: int, *, q_norm=None, k_norm=None, pos: torch.Tensor | None = None,
+                rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None, innovation: bool = True,
+                pooled_v: bool = False):
+    """``pack_qkv`` with V packed straight into attention tiles and the
+    block-mean pooling of the patch tokens in the same pass.
+
+    Returns ``(q_patch, q_special, k, vt, pooled_q, pooled_k, innovation,
+    pooled_v)``: ``q_patch`` / ``q_special`` / ``k`` as ``pack_qkv`` (bit
+    for bit), ``vt`` as ``pack_v`` of the packed V, ``pooled_q`` / ``pooled_k``
+    as ``pool_qkv(q_patch, k[:, :, :Np])``, ``innovation`` (or None) the pair
+    innovation of the patch values' block means, ``pooled_v`` (or None) those
+    means. Requires at least one patch token per frame.
+    """
+    B, T, H, D = q.shape
+    N, P, S = int(frames), int(tokens_per_frame), int(special)
+    if N * P != T or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q/k/v must be [B,{N}*{P},H,D], got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if not 0 <= S < P:
+        raise ValueError(f"frames of {P} tokens need at least one patch token (special={S})")
+    dev = q.device
+    n_patch = N * (P - S)
+    kb = math.ceil(n_patch / BLOCK_K)
+    bf = dict(device=dev, dtype=torch.bfloat16)
+    qp = torch.empty(B, H, n_patch, D, **bf)
+    qs = torch.empty(B, H, N * S, D, **bf)
+    ko = torch.empty(B, H, T, D, **bf)
+    vt = torch.empty(B, H, math.ceil(T / BLOCK_K), D, BLOCK_K, **bf)
+    pq = torch.empty(B, H, math.ceil(n_patch / BLOCK_Q), D, **bf)
+    pk = torch.empty(B, H, kb, D, **bf)
+    pv = torch.empty(B, H, kb, D, **bf) if pooled_v else None
+    inn = torch.empty(B, H, (kb + 1) // 2, device=dev, dtype=torch.float32) if innovation else None
+    keep, args = _layout_args(B, T, D, q_norm, k_norm, pos, rope_tables)
+    _lib.call("vasc_pack_global", *_btht(q, "q"), *_btht(k, "k"), *_btht(v, "v"), B, H, N, P, S, D, *args,
+              qp.data_ptr(), qs.data_ptr(), ko.data_ptr(), vt.data_ptr(), pq.data_ptr(), pk.data_ptr(), _ptr(pv),
+              _ptr(inn), _stream())
+    del keep
+    return qp, (qs if S else None), ko, vt, pq, pk, inn, pv
 
 
 def restore_tokens(x_patch: torch.Tensor, x_special: torch.Tensor | None, frames: int, tokens_per_frame: int,

@@ -448,7 +448,8 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
     the patch values when the caller pooled them already."""
     _check_research_kwargs(research)
     for t, name in ((key, "key"), (value, "value"), (pooled_score, "pooled_score")):
-        _require_gpu(t, name)
+        if t is not None:
+            _require_gpu(t, name)
     cfg = routing_config()
     Tk = key.shape[-2]
     orig_kblk = pooled_score.shape[-1]
@@ -471,6 +472,8 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
         B, H = pooled_score.shape[:2]
         P = (orig_kblk + 1) // 2
         if innovation is None:
+            if value is None:
+                raise ValueError("CoSA pair debt requires the values or their pair innovation")
             _, _, _, innovation = ops.pool_qkv(v=value[..., :num_patch_tokens, :])
         if base is not None:
             # no hint with a cdf threshold: M is the largest row capacity (SW:3709-3712)
@@ -563,7 +566,7 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
                             routing_stats_store: dict | None = None, routing_state: dict | None = None,
                             num_patch_tokens: int | None = None, want_sparsity: bool = True,
                             _innovation: torch.Tensor | None = None, token_layout: tuple | None = None,
-                            **research):
+                            _vt: torch.Tensor | None = None, **research):
     """``block_sparse_attn_cuda`` for a whole global layer: the selection of
     the patch queries as there, and the special-token queries (which the
     reference runs through a dense SDPA, ATT:8464-8484) over every key in
@@ -573,12 +576,15 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
     innovation when the caller pooled them with Q and K). With
     ``token_layout = (N, P, S)`` the first result is instead the layer's
     frame-major ``[B, N*P, H*D]`` output (restore included) and the second
-    None."""
+    None. ``_vt``: the values already packed as ``ops.pack_v(value)`` (then
+    ``value`` may be None)."""
     _require_gpu(q_patch, "query")
+    if value is None and _vt is None:
+        raise ValueError("sparse_global_attention requires the values (or their packed tiles)")
     sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
                                         routing_stats_store, routing_state, num_patch_tokens, research,
                                         innovation=_innovation)
-    vt = ops.pack_v(value)
+    vt = ops.pack_v(value) if _vt is None else _vt
     thr = _pv_threshold(key, layer_idx)
     if thr is None:
         if token_layout is not None:
