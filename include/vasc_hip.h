@@ -86,8 +86,12 @@ int vasc_pool_qk_max(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st
  * i.e. the score/softmax of predict_attention (attention.py:97-101) with the
  * roundings of its bf16 autocast matmul. round_bf16 = 0 skips both
  * bfloat16 roundings. pooled_q [B,H,qb,d], pooled_k [B,H,kb,d] contiguous;
- * prob [B,H,qb,kb] float32 contiguous; scale finite and > 0. workspace: at
- * least vasc_pooled_softmax_workspace_size(B, H, qb, kb) bytes, 8-byte
+ * prob [B,H,qb,kb] float32 contiguous; scale finite and > 0. priority:
+ * NULL, or a second [B,H,qb,kb] output receiving max(prob, 0) with NaN -> 0,
+ * the VASC ledger's QK-order priority (sparse_wrapper.py:3680-3684, 4030).
+ * kb <= 1280: one launch (a workgroup holds 32 query rows against every
+ * key in registers) and no workspace (NULL allowed). Larger kb: workspace
+ * of at least vasc_pooled_softmax_workspace_size(B, H, qb, kb) bytes, 8-byte
  * aligned (per-row softmax states of each 256-key block, written by a first
  * kernel and merged by the second; no state is kept between calls).
  * Built variant: d == 64; kb < 2^22.
@@ -95,10 +99,10 @@ int vasc_pool_qk_max(const uint16_t *q, int64_t q_sb, int64_t q_sh, int64_t q_st
 int vasc_pooled_softmax(const uint16_t *pooled_q, const uint16_t *pooled_k,
                         int64_t B, int64_t H, int64_t qb, int64_t kb, int64_t d,
                         float scale, int32_t round_bf16, float *prob,
-                        void *workspace, void *stream);
+                        float *priority, void *workspace, void *stream);
 
 /* Bytes of the vasc_pooled_softmax workspace (B*H*ceil(kb/256)*qb*8); 0 for
- * empty shapes. Host-only. */
+ * empty shapes and for kb <= 1280 (no workspace). Host-only. */
 int64_t vasc_pooled_softmax_workspace_size(int64_t B, int64_t H, int64_t qb, int64_t kb);
 
 /*

@@ -425,6 +425,10 @@ def test_global_layer_vasc_chain_matches_oracle(backbone, monkeypatch):
         err = (out.float() - ref).abs()
         assert err.max() < 6e-2 and err.mean() < 6e-3, (layer, err.max().item(), err.mean().item())
     assert "cosa_value_risk_pair_debt" in routing_state
+    # the ledger's QK-order priority is the last layer's cleaned score
+    last = recorded[-1]["prob"]
+    prio = routing_state["cosa_value_risk_pair_qk_order_priority"]
+    assert torch.equal(prio.view(torch.int32), torch.where(last > 0, last, 0.0).view(torch.int32))
 
 
 def test_pack_norm_parameters_bf16_and_updated_through_data():

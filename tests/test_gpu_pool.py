@@ -91,6 +91,22 @@ def test_pooled_softmax(qb, kb):
     assert np.isclose(p16, ref16, rtol=2e-5, atol=1e-9).mean() > 0.99
 
 
+@pytest.mark.parametrize("qb,kb", [(40, 256), (70, 257), (33, 1280), (33, 1281), (9, 2082)])
+def test_pooled_softmax_paths_and_priority(qb, kb):
+    """Both launch shapes (one launch up to 1280 key blocks, the two-kernel
+    path beyond) stay inside the element-wise bound, and the priority output
+    is the cleaned probability, bit for bit."""
+    from vasc_amd import ops
+    pq, pk = _rand((1, 2, qb, 64), kb) * 3, _rand((1, 2, kb, 64), kb + 1) * 3
+    prob, prio = ops.pooled_softmax(pq.cuda(), pk.cuda(), priority=True)
+    prob, prio = prob.cpu(), prio.cpu()
+    out = OP.prob_outside_bound(prob.numpy(), pq.float().numpy(), pk.float().numpy(), bf16=True)
+    assert not out.any(), f"{out.sum()} of {out.size} outside the one-step logit bound"
+    assert np.allclose(prob.sum(-1).numpy(), 1.0, atol=1e-5)
+    assert torch.equal(prio.view(torch.int32), torch.where(prob > 0, prob, 0.0).view(torch.int32))
+    assert torch.equal(ops.pooled_softmax(pq.cuda(), pk.cuda()).cpu().view(torch.int32), prob.view(torch.int32))
+
+
 def _softmax_ref(pq, pk, scale, rnd):
     dots = np.einsum("...qd,...kd->...qk", pq.float().numpy().astype(np.float64),
                      pk.float().numpy().astype(np.float64)).astype(np.float32)

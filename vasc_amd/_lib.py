@@ -33,7 +33,7 @@ SIGNATURES: dict[str, tuple] = {
                                   P, P, P]),
     "vasc_pool_qkv": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64,
                                 I64, I64, I64, I64, I64, I64, I64, P, P, P, P, P]),
-    "vasc_pooled_softmax": (c_int32, [P, P, I64, I64, I64, I64, I64, c_float, I32, P, P, P]),
+    "vasc_pooled_softmax": (c_int32, [P, P, I64, I64, I64, I64, I64, c_float, I32, P, P, P, P]),
     "vasc_pooled_softmax_workspace_size": (I64, [I64, I64, I64, I64]),
     "vasc_pair_innovation": (c_int32, [P, I64, I64, I64, I64, P, P]),
     "vasc_select_workspace_size": (c_size_t, [I64, I64, I64, I64]),

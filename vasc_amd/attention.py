@@ -127,12 +127,14 @@ def adaptive_sparse_attention_forward(self, x: torch.Tensor, pos: torch.Tensor, 
             qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], N, P, S, q_norm=layer_norm_args(self.q_norm),
             k_norm=layer_norm_args(self.k_norm), pos=pos if rope is not None else None, rope_tables=tables,
             innovation=vasc_mode)
-        attn_pooled = ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(hd))
+        # the ledger's QK-order priority (the cleaned score) from the same launch
+        attn_pooled, priority = ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(hd), priority=True) \
+            if vasc_mode else (ops.pooled_softmax(pq, pk, scale=1.0 / math.sqrt(hd)), None)
         tokens_out, _, sparsity = sparse_global_attention(
             q_patch, q_special, k_re, None, attn_pooled, sparse_ratio=sparse_ratio, cdf_threshold=cdf_threshold,
             layer_idx=layer_idx, routing_state=routing_state, num_patch_tokens=n_patch,
             want_sparsity=aux_output_store is not None, _innovation=innovation, token_layout=(N, P, S), _vt=vt,
-            **research)
+            _priority=priority, **research)
         return _finish(self, x, tokens_out, sparsity, aux_output_store)
     if fused_layout_supported(self):
         tables = rope.tables(hd, x.device) if rope is not None else None

@@ -229,6 +229,7 @@ struct BlockParams {
   const uint16_t *pq, *pk;
   float2 *part;  // [B*H][nkb][qb] per-block row states (max y, sum exp2(y - max))
   float *prob;
+  float *priority;  // optional: max(prob, 0) with NaN -> 0
   int64_t qb, kb, nrb, nkb, num_wg;
   float scale, sc;
 };
@@ -381,6 +382,9 @@ __global__ __launch_bounds__(kBlockWaves * 64) void pooled_prob_kernel(const Blo
   float *base = p.prob + (c.bh * p.qb + c.R0) * p.kb + c.key0;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       base, 0, static_cast<int>((static_cast<int64_t>(c.rows - 1) * p.kb + c.nkeys) * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t prio = __builtin_amdgcn_make_buffer_rsrc(
+      p.priority ? p.priority + (base - p.prob) : base, 0,
+      p.priority ? static_cast<int>((static_cast<int64_t>(c.rows - 1) * p.kb + c.nkeys) * 4) : 0, 0x00020000);
   uint32_t soff[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) soff[r] = static_cast<uint32_t>(acc_row(r, 0) * kb * 4);
@@ -412,8 +416,155 @@ __global__ __launch_bounds__(kBlockWaves * 64) void pooled_prob_kernel(const Blo
       // (below 2^31) with or without the scalar row offset: the store is dropped
       const bool ok = full || (kok && acc_row(r, 0) < rlim);
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pr), rsrc, ok ? voff : 0x80000000u, soff[r], 0);
+      // a null priority has a zero-size range: the store is dropped
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pr > 0.f ? pr : 0.f), prio, ok ? voff : 0x80000000u,
+                                            soff[r], 0);
     }
   }
+}
+
+// One launch for rows of at most 256 kTiles keys: workgroup g takes the 32
+// pooled query rows 32 (g % nrt) .. of head g / nrt against every key of the
+// head. Wave w holds the key tiles w, w + 8, .. (32 keys each) as the
+// accumulators of S = Q K^T (lane = key, accumulators = rows), so each logit
+// is computed once and stays in registers: the row maxima are reduced across
+// the 32 lanes of a half and then the eight waves through LDS, the row sums
+// of exp2(y - max) likewise, and the normalised probabilities are written
+// from the same registers (a store covers two rows of 32 consecutive keys).
+// Needs no workspace.
+template <int kMode, int kTiles>
+__global__ __launch_bounds__(kBlockWaves * 64) void pooled_rows_kernel(const BlockParams p) {
+  __shared__ float red[kBlockWaves][32];
+  __shared__ __attribute__((aligned(16))) float rowv[32];
+  const int tid = threadIdx.x, l = tid & 63, lr = l & 31, hf = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t wg = xcd_remap(blockIdx.x, p.num_wg);
+  const int64_t bh = wg / p.nrb;
+  const int64_t R0 = (wg % p.nrb) * 32;
+  const int rows = static_cast<int>(p.qb - R0 < 32 ? p.qb - R0 : 32);
+  const int kb = static_cast<int>(p.kb);
+  u32x4 qt[4], kt[kTiles][4];
+  {
+    const uint16_t *qr = p.pq + (bh * p.qb + R0 + (lr < rows ? lr : 0)) * kHeadDim + 8 * hf;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qt[s] = *reinterpret_cast<const u32x4 *>(qr + 16 * s);
+  }
+#pragma unroll
+  for (int i = 0; i < kTiles; ++i) {
+    const int key0 = 32 * (w + kBlockWaves * i);
+    if (key0 >= kb) break;
+    const int key = key0 + lr < kb ? key0 + lr : key0;
+    const uint16_t *kr = p.pk + (bh * p.kb + key) * kHeadDim + 8 * hf;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kt[i][s] = *reinterpret_cast<const u32x4 *>(kr + 16 * s);
+  }
+  floatx16 acc[kTiles];
+  float m[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) m[r] = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kTiles; ++i) {
+    const int key0 = 32 * (w + kBlockWaves * i);
+    if (key0 < kb) {
+      acc[i] = tile_dots(qt, kt[i]);
+      dots_to_r<kMode>(acc[i], p.scale);
+      if (key0 + lr >= kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = -INFINITY;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m[r] = fmaxf(m[r], acc[i][r]);
+  }
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m[r] = fmaxf(m[r], xor_lane(m[r], off));
+  if (lr == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[w][acc_row(r, hf)] = m[r];
+  }
+  __syncthreads();
+  if (tid < 32) {
+    float g = red[0][tid];
+#pragma unroll
+    for (int i = 1; i < kBlockWaves; ++i) g = fmaxf(g, red[i][tid]);
+    rowv[tid] = g * p.sc;  // the row's largest exp2 argument
+  }
+  __syncthreads();
+  float gm[16];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const floatx4 m4 = *reinterpret_cast<const floatx4 *>(rowv + 8 * g + 4 * hf);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gm[4 * g + e] = m4[e];
+  }
+  float sum[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sum[r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < kTiles; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc[i][r] = __builtin_amdgcn_exp2f(fmaf(acc[i][r], p.sc, -gm[r]));
+      sum[r] += acc[i][r];
+    }
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sum[r] += xor_lane(sum[r], off);
+  if (lr == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[w][acc_row(r, hf)] = sum[r];
+  }
+  __syncthreads();
+  if (tid < 32) {
+    float t = red[0][tid];
+#pragma unroll
+    for (int i = 1; i < kBlockWaves; ++i) t += red[i][tid];
+    rowv[tid] = 1.f / t;
+  }
+  __syncthreads();
+  float inv[16];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const floatx4 i4 = *reinterpret_cast<const floatx4 *>(rowv + 8 * g + 4 * hf);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) inv[4 * g + e] = i4[e];
+  }
+  float *base = p.prob + (bh * p.qb + R0) * p.kb;
+  const int bytes = rows * kb * 4;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t prio = __builtin_amdgcn_make_buffer_rsrc(
+      p.priority ? p.priority + (bh * p.qb + R0) * p.kb : base, 0, p.priority ? bytes : 0, 0x00020000);
+  const int rlim = rows - 4 * hf;  // row acc_row(r, hf) < rows <=> acc_row(r, 0) < rlim
+#pragma unroll
+  for (int i = 0; i < kTiles; ++i) {
+    const int key0 = 32 * (w + kBlockWaves * i);
+    if (key0 >= kb) break;
+    const bool kok = key0 + lr < kb;
+    const uint32_t voff = static_cast<uint32_t>(((4 * hf) * kb + key0 + lr) * 4);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pr = acc[i][r] * inv[r];
+      // rows past qb and keys past kb: an offset of 2^31 lies past the range
+      const uint32_t off = kok && acc_row(r, 0) < rlim ? voff : 0x80000000u;
+      const uint32_t soff = static_cast<uint32_t>(acc_row(r, 0) * kb * 4);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pr), rsrc, off, soff, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pr > 0.f ? pr : 0.f), prio, off, soff, 0);
+    }
+  }
+}
+
+// key tiles per wave of pooled_rows_kernel for kb keys (0: the two-kernel path)
+constexpr int kRowTileSteps[] = {1, 2, 3, 5};
+inline int row_tiles(int64_t kb) {
+  for (int t : kRowTileSteps)
+    if (kb <= 32 * kBlockWaves * t) return t;
+  return 0;
 }
 
 }  // namespace
@@ -507,16 +658,19 @@ extern "C" int vasc_pair_innovation(const float *pooled_v, int64_t B, int64_t H,
 
 extern "C" int64_t vasc_pooled_softmax_workspace_size(int64_t B, int64_t H, int64_t qb, int64_t kb) {
   using namespace vasc;
+  if (row_tiles(kb)) return 0;  // one launch, no row states
   return B > 0 && H > 0 && qb > 0 && kb > 0 ? B * H * cdiv(kb, kBlockKeys) * qb * 8 : 0;
 }
 
 extern "C" int vasc_pooled_softmax(const uint16_t *pooled_q, const uint16_t *pooled_k, int64_t B, int64_t H,
                                    int64_t qb, int64_t kb, int64_t d, float scale, int32_t round_bf16, float *prob,
-                                   void *workspace, void *stream) {
+                                   float *priority, void *workspace, void *stream) {
   using namespace vasc;
   VASC_SUPPORTED(d == 64, "head_dim %lld not built (built: 64)", (long long)d);
-  VASC_REQUIRE(pooled_q && pooled_k && prob && workspace && B > 0 && H > 0 && qb > 0 && kb > 0,
-               "invalid arguments (pooled_q, pooled_k, prob and workspace are required)");
+  const int tiles = row_tiles(kb);
+  VASC_REQUIRE(pooled_q && pooled_k && prob && (workspace || tiles) && B > 0 && H > 0 && qb > 0 && kb > 0,
+               "invalid arguments (pooled_q, pooled_k, prob and, for kb > %d, workspace are required)",
+               32 * kBlockWaves * kRowTileSteps[3]);
   VASC_REQUIRE(std::isfinite(scale) && scale > 0.f, "scale must be finite and positive");
   VASC_REQUIRE((reinterpret_cast<uintptr_t>(pooled_q) & 15) == 0 && (reinterpret_cast<uintptr_t>(pooled_k) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(workspace) & 7) == 0,
@@ -528,18 +682,36 @@ extern "C" int vasc_pooled_softmax(const uint16_t *pooled_q, const uint16_t *poo
   p.pk = pooled_k;
   p.part = static_cast<float2 *>(workspace);
   p.prob = prob;
+  p.priority = priority;
   p.qb = qb;
   p.kb = kb;
-  p.nrb = cdiv(qb, kBlockRows);
-  p.nkb = cdiv(kb, kBlockKeys);
-  p.num_wg = p.nrb * p.nkb * B * H;
-  VASC_REQUIRE(p.num_wg < (int64_t(1) << 31), "grid too large");
   int e = 0;
   const bool pow2 = std::frexp(scale, &e) == 0.5f;
   const int mode = !round_bf16 ? kFp32 : pow2 ? kRoundPow2 : kRoundAny;
   p.scale = scale;
   p.sc = mode == kRoundAny ? kLog2e : scale * kLog2e;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (tiles) {
+    p.nrb = cdiv(qb, 32);
+    p.nkb = 1;
+    p.num_wg = p.nrb * B * H;
+    VASC_REQUIRE(p.num_wg < (int64_t(1) << 31), "grid too large");
+    using Kern = void (*)(BlockParams);
+    static constexpr Kern kRows[3][4] = {
+        {pooled_rows_kernel<kRoundPow2, 1>, pooled_rows_kernel<kRoundPow2, 2>, pooled_rows_kernel<kRoundPow2, 3>,
+         pooled_rows_kernel<kRoundPow2, 5>},
+        {pooled_rows_kernel<kRoundAny, 1>, pooled_rows_kernel<kRoundAny, 2>, pooled_rows_kernel<kRoundAny, 3>,
+         pooled_rows_kernel<kRoundAny, 5>},
+        {pooled_rows_kernel<kFp32, 1>, pooled_rows_kernel<kFp32, 2>, pooled_rows_kernel<kFp32, 3>,
+         pooled_rows_kernel<kFp32, 5>}};
+    const int ti = tiles == 1 ? 0 : tiles == 2 ? 1 : tiles == 3 ? 2 : 3;
+    hipLaunchKernelGGL(kRows[mode][ti], dim3(p.num_wg), dim3(kBlockWaves * 64), 0, st, p);
+    return check_launch("vasc_pooled_softmax");
+  }
+  p.nrb = cdiv(qb, kBlockRows);
+  p.nkb = cdiv(kb, kBlockKeys);
+  p.num_wg = p.nrb * p.nkb * B * H;
+  VASC_REQUIRE(p.num_wg < (int64_t(1) << 31), "grid too large");
   auto ks = mode == kRoundPow2 ? pooled_stats_kernel<kRoundPow2>
             : mode == kRoundAny ? pooled_stats_kernel<kRoundAny>
                                 : pooled_stats_kernel<kFp32>;

@@ -85,8 +85,13 @@ def pool_qkv(q=None, k=None, v=None, *, innovation: bool = True):
 
 
 def pooled_softmax(pooled_q: torch.Tensor, pooled_k: torch.Tensor, *, scale: float | None = None,
-                   round_bf16: bool = True) -> torch.Tensor:
-    """fp32 ``softmax(bf16(bf16(pq.pk) * scale))`` over key blocks, ``[B,H,Qb,Kb]``."""
+                   round_bf16: bool = True, priority: bool = False):
+    """fp32 ``softmax(bf16(bf16(pq.pk) * scale))`` over key blocks, ``[B,H,Qb,Kb]``.
+
+    ``priority=True`` returns ``(prob, priority)`` with ``priority`` the
+    VASC ledger's QK-order priority ``max(prob, 0)``, NaN -> 0, written by
+    the same launch.
+    """
     _dev(pooled_q, "pooled_q")
     _dev(pooled_k, "pooled_k")
     pq = pooled_q.to(torch.bfloat16).contiguous()
@@ -95,10 +100,12 @@ def pooled_softmax(pooled_q: torch.Tensor, pooled_k: torch.Tensor, *, scale: flo
     kb = pk.shape[2]
     scale = 1.0 / math.sqrt(D) if scale is None else scale
     prob = torch.empty(B, H, qb, kb, device=pq.device, dtype=torch.float32)
-    ws = torch.empty(_lib.load().vasc_pooled_softmax_workspace_size(B, H, qb, kb), device=pq.device, dtype=torch.uint8)
+    prio = torch.empty_like(prob) if priority else None
+    size = _lib.load().vasc_pooled_softmax_workspace_size(B, H, qb, kb)
+    ws = torch.empty(size, device=pq.device, dtype=torch.uint8) if size else None
     _lib.call("vasc_pooled_softmax", pq.data_ptr(), pk.data_ptr(), B, H, qb, kb, D, float(scale),
-              int(bool(round_bf16)), prob.data_ptr(), ws.data_ptr(), _stream())
-    return prob
+              int(bool(round_bf16)), prob.data_ptr(), _ptr(prio), _ptr(ws), _stream())
+    return (prob, prio) if priority else prob
 
 
 def pair_innovation(pooled_value: torch.Tensor) -> torch.Tensor:

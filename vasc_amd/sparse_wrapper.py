@@ -169,10 +169,11 @@ def _service_domain() -> str:
 
 
 def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_idx: int, M: int,
-                    domain: str = "qk_admission") -> None:
+                    domain: str = "qk_admission", priority: torch.Tensor | None = None) -> None:
     """State writes of the selector (SW:3990-4025). In the QK-admission domain
     the service observation is recorded here; in the PV-execution domain the
-    attention launch records it (``_record_pv_execution``)."""
+    attention launch records it (``_record_pv_execution``). ``priority``: the
+    cleaned score when the pooled softmax already wrote it."""
     B, H, Q, K = score.shape
     P = (K + 1) // 2
     routing_state[STATE_KEY] = out["debt"].view(B, H, 1, P)
@@ -193,8 +194,10 @@ def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_i
     routing_state["cosa_value_risk_pair_max_patch_blocks"] = int(M)
     routing_state["cosa_value_risk_pair_selected_indices"] = out["index"][..., :M]
     # clamp_min(0) then NaN -> 0, as the reference's score (SW:3680-3684), in one pass
-    sf = score.float()
-    routing_state["cosa_value_risk_pair_qk_order_priority"] = torch.where(sf > 0, sf, 0.0)
+    if priority is None:
+        sf = score.float()
+        priority = torch.where(sf > 0, sf, 0.0)
+    routing_state["cosa_value_risk_pair_qk_order_priority"] = priority
 
 
 def _pv_execution_service(pv_map: torch.Tensor, patch_blocks: int) -> torch.Tensor:
@@ -441,11 +444,13 @@ def _check_research_kwargs(kwargs: dict) -> None:
 
 def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torch.Tensor, topk, sparse_ratio,
                       cdf_threshold, layer_idx: int, routing_stats_store, routing_state, num_patch_tokens,
-                      research: dict, innovation: torch.Tensor | None = None):
+                      research: dict, innovation: torch.Tensor | None = None,
+                      priority: torch.Tensor | None = None):
     """Mode switch, budget, mixed-tail and sink rules and kernel 2 of
     block_sparse_attn_cuda (SW:6998-7041, 7559-7770). Returns the selection
     and the total key-block count. ``innovation``: the pair innovation of
-    the patch values when the caller pooled them already."""
+    the patch values when the caller pooled them already; ``priority``: the
+    cleaned score when the caller's softmax wrote it."""
     _check_research_kwargs(research)
     for t, name in ((key, "key"), (value, "value"), (pooled_score, "pooled_score")):
         if t is not None:
@@ -489,7 +494,7 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
                                 pending_arrival=pending, prev_service=service,
                                 want_priority=not cfg.skip_routing_stats, want_mask=want_stats)
         M = min(hint, orig_kblk)
-        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, M, cfg.service_domain)
+        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, M, cfg.service_domain, priority)
         if want_stats:
             # the base map the reference hands its selector: Top-K (or the
             # cdf counts) plus the forced mixed tail (SW:7599-7662, 7750-7762)
@@ -566,7 +571,8 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
                             routing_stats_store: dict | None = None, routing_state: dict | None = None,
                             num_patch_tokens: int | None = None, want_sparsity: bool = True,
                             _innovation: torch.Tensor | None = None, token_layout: tuple | None = None,
-                            _vt: torch.Tensor | None = None, **research):
+                            _vt: torch.Tensor | None = None, _priority: torch.Tensor | None = None,
+                            **research):
     """``block_sparse_attn_cuda`` for a whole global layer: the selection of
     the patch queries as there, and the special-token queries (which the
     reference runs through a dense SDPA, ATT:8464-8484) over every key in
@@ -577,13 +583,14 @@ def sparse_global_attention(q_patch: torch.Tensor, q_special: torch.Tensor | Non
     ``token_layout = (N, P, S)`` the first result is instead the layer's
     frame-major ``[B, N*P, H*D]`` output (restore included) and the second
     None. ``_vt``: the values already packed as ``ops.pack_v(value)`` (then
-    ``value`` may be None)."""
+    ``value`` may be None); ``_priority``: ``pooled_score`` cleaned as the
+    ledger stores it (``ops.pooled_softmax(..., priority=True)``)."""
     _require_gpu(q_patch, "query")
     if value is None and _vt is None:
         raise ValueError("sparse_global_attention requires the values (or their packed tiles)")
     sel, total_kblk = _select_for_layer(key, value, pooled_score, topk, sparse_ratio, cdf_threshold, layer_idx,
                                         routing_stats_store, routing_state, num_patch_tokens, research,
-                                        innovation=_innovation)
+                                        innovation=_innovation, priority=_priority)
     vt = ops.pack_v(value) if _vt is None else _vt
     thr = _pv_threshold(key, layer_idx)
     if thr is None:
