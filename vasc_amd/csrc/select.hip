@@ -1240,9 +1240,11 @@ constexpr int kRowWaveWords = 320 + 128 + 64 * kSeg;
 
 // The threshold of the keys of a padded row (64 EPT keys, 0 the smallest
 // any element can have, held by the padding): keys > T are kept, keys == T
-// in index order up to need (eqT of them). A histogram of a sample (lanes 4i
-// of the even slots; 256 bins over the sampled keys' range above 0)
-// brackets the c-th largest key at its sample rank c S / n -+ 3 sigma + 1;
+// in index order up to need (eqT of them). A histogram of a sample (every
+// lane's even slots; 256 bins over the sampled keys' range above 0)
+// brackets the c-th largest key at its sample rank c S / n -+ 3 sigma + 1
+// (half the keys sampled: about 2 n 3 sqrt(f (1 - f) / S) candidates, which
+// at 4096 keys and f = c / n = 1/4 stays well under kSeg per lane);
 // keys above the bracket are kept, the bracket's keys are staged per lane
 // and ranked exactly (rank_segs). When fewer than c keys exceed 0 the
 // threshold is 0, its ties going in index order. When the bracket misses,
@@ -1252,16 +1254,15 @@ template <int EPT>
 __device__ __forceinline__ void rows_threshold(const uint32_t (&key)[EPT], int lane, int c, uint32_t *hist,
                                                uint32_t *sbuf, uint32_t *cand, uint32_t &T, int &need, int &eqT) {
   constexpr int n = 64 * EPT;
-  constexpr int S = 16 * ((EPT + 1) / 2);  // samples
-  const bool sampler = (lane & 3) == 0;
+  constexpr int S = 64 * ((EPT + 1) / 2);  // samples
   uint32_t smin = 0xffffffffu, smax = 0u;  // smin: over sampled keys above 0, less one
 #pragma unroll
   for (int m = 0; m < EPT; m += 2) {
-    smin = min(smin, sampler ? key[m] - 1u : 0xffffffffu);
-    smax = max(smax, sampler ? key[m] : 0u);
+    smin = min(smin, key[m] - 1u);
+    smax = max(smax, key[m]);
   }
 #pragma unroll
-  for (int o = 32; o >= 4; o >>= 1) {
+  for (int o = 32; o >= 1; o >>= 1) {
     smin = min(smin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(smin), o)));
     smax = max(smax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(smax), o)));
   }
@@ -1275,10 +1276,8 @@ __device__ __forceinline__ void rows_threshold(const uint32_t (&key)[EPT], int l
     const int sh = 32 - __clz(range) > 8 ? 32 - __clz(range) - 8 : 0;
     *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
     wave_sync();
-    if (sampler) {
 #pragma unroll
-      for (int m = 0; m < EPT; m += 2) atomicAdd(&hist[key[m] ? (key[m] - smin) >> sh : 256u + lane], 1u);
-    }
+    for (int m = 0; m < EPT; m += 2) atomicAdd(&hist[key[m] ? (key[m] - smin) >> sh : 256u + lane], 1u);
     wave_sync();
     u32x4 h;
     const int suf = hist_suffix(hist, lane, h);
@@ -1487,30 +1486,39 @@ void select_rows_kernel(const SelectParams p, int rows_per_wave) {
     const __amdgpu_buffer_rsrc_t irs =
         __builtin_amdgcn_make_buffer_rsrc(p.index_out + row * p.width, 0, static_cast<int>(4 * p.width), 0x00020000);
     uint32_t *cnt_l = pair_cnt + (lane >> 1);
-    int base = 0, run_eq = 0;
-#pragma unroll
-    for (int m = 0; m < EPT; ++m) {
-      const uint32_t xk = key[m];
-      bool sel;
-      if (!split) {
-        sel = xk >= T;
-      } else {
-        const bool eq = xk == T;
-        const uint64_t beq = __builtin_amdgcn_ballot_w64(eq);
-        sel = xk > T || (eq && run_eq + lanes_below(beq) < need);
-        run_eq += __popcll(beq);
-      }
+    int base = 0;
+    // one element slot: its ballot, the store (unselected lanes store past
+    // the buffer range, which drops them) and the pair count; the lane's
+    // position is computed by every lane (no exec-masked block per slot)
+    auto emit = [&](int m, bool sel) {
       const uint64_t bm = __builtin_amdgcn_ballot_w64(sel);
-      // unselected lanes store past the buffer range (dropped)
+      int pos = lanes_below(bm);
+      asm volatile("" : "+v"(pos));
       __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(lane + 64 * m), irs,
-                                            sel ? 4 * (base + lanes_below(bm)) : 0x7ffffff0, 0, 0);
+                                            sel ? 4 * (base + pos) : 0x7ffffff0u, 0, 0);
       if (kVasc) atomicAdd(&cnt_l[32 * m], sel ? 1u : 0u);
       base += __popcll(bm);
+    };
+    if (!split) {
+#pragma unroll
+      for (int m = 0; m < EPT; ++m) emit(m, key[m] >= T);
+    } else {
+      int run_eq = 0;
+#pragma unroll
+      for (int m = 0; m < EPT; ++m) {
+        const uint32_t xk = key[m];
+        const bool eq = xk == T;
+        const uint64_t beq = __builtin_amdgcn_ballot_w64(eq);
+        int below = lanes_below(beq);
+        asm volatile("" : "+v"(below));
+        emit(m, xk > T || (eq && run_eq + below < need));
+        run_eq += __popcll(beq);
+      }
     }
     if (p.mask_out) {
       uint8_t *mrow = p.mask_out + row * p.K;
       const int ln = opaque_lane(lane);
-      run_eq = 0;
+      int run_eq = 0;
 #pragma unroll
       for (int m = 0; m < EPT; ++m) {
         const int k = ln + 64 * m;
