@@ -34,7 +34,8 @@ SOURCES = {
     # no NaN canonicalisation around the running max.
     "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
     "pack.hip": [],
-    # the rotary embedding rounds its products and sum separately, as torch does
+    # products and sums round separately except where the code fuses them
+    # explicitly (fmaf in the LayerNorm and rotary of transform_row)
     "layout.hip": ["-ffp-contract=off"],
     "pool.hip": ["-ffp-contract=off"],
     "select.hip": ["-ffp-contract=off", "-Wshadow"],

@@ -92,19 +92,24 @@ __device__ __forceinline__ void transform_row(const PackParams &p, const floatx4
     const floatx4 w0 = nrm[pn][0][2 * sub], w1 = nrm[pn][0][2 * sub + 1];
     const floatx4 b0 = nrm[pn][1][2 * sub], b1 = nrm[pn][1][2 * sub + 1];
     const float eps = part == 0 ? p.eps[0] : p.eps[1];
+    // statistics in float32 with fused multiply-adds and the hardware
+    // reciprocal square root (about one ulp): the output is rounded to bf16
     float s = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) s += x[e];
-    const float mean = group8_sum(s) / static_cast<float>(kHeadDim);
+    const float mean = group8_sum(s) * (1.0f / kHeadDim);
     float v = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v += (x[e] - mean) * (x[e] - mean);
-    const float var = group8_sum(v) / static_cast<float>(kHeadDim);
-    const float rstd = 1.0f / sqrtf(var + eps);
+    for (int e = 0; e < 8; ++e) {
+      x[e] -= mean;
+      v = fmaf(x[e], x[e], v);
+    }
+    const float var = group8_sum(v) * (1.0f / kHeadDim);
+    const float rstd = __builtin_amdgcn_rsqf(var + eps);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float we = e < 4 ? w0[e] : w1[e - 4], be = e < 4 ? b0[e] : b1[e - 4];
-      x[e] = ((x[e] - mean) * rstd) * we + be;
+      x[e] = fmaf(x[e] * rstd, we, be);
     }
   }
   if (rope) {
@@ -120,7 +125,7 @@ __device__ __forceinline__ void transform_row(const PackParams &p, const floatx4
       const float partner = dpp<kQuadXor2>(x[e]);
       const float rot = first ? -partner : partner;
       const float ce = e < 4 ? c0[e] : c1[e - 4], se = e < 4 ? s0[e] : s1[e - 4];
-      x[e] = x[e] * ce + rot * se;
+      x[e] = fmaf(rot, se, x[e] * ce);
     }
   }
 }
@@ -294,22 +299,32 @@ __global__ __launch_bounds__(kThreads) void pack_global_kernel(const PackParams 
       }
     }
   }
-  // sums across the 8 row groups of the wave (lane bits 3-5), then per wave to LDS
+  // Sums of the 40 partials (flat index 8 j + e) across the 8 row groups of
+  // the wave (lane bits 3-5), reduced and scattered at once: a 32-lane
+  // permlane swap of partials i and i + 20 leaves the lower lanes summing
+  // i and the upper lanes i + 20, a 16-lane swap of i and i + 10 splits
+  // again, and a DPP row rotate by 8 finishes. Lane bits 5 and 4 then name
+  // the ten partials a lane holds (flat index t + 10 b4 + 20 b5).
+  float g[20], hs[10];
 #pragma unroll
-  for (int j = 0; j < 5; ++j)
+  for (int i = 0; i < 20; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i >> 3][i & 7]),
+                                                    __float_as_uint(acc[(i + 20) >> 3][(i + 20) & 7]), false, false);
+    g[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = acc[j][e];
-      v += xor_lane(v, 8);
-      v += xor_lane(v, 16);
-      v += xor_lane(v, 32);
-      acc[j][e] = v;
+  for (int i = 0; i < 10; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(g[i]), __float_as_uint(g[i + 10]), false, false);
+    hs[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    hs[i] += xor_lane(hs[i], 8);
+  }
+  if ((lane & 8) == 0) {
+    const int first = 10 * ((lane >> 4) & 1) + 20 * (lane >> 5);
+#pragma unroll
+    for (int t = 0; t < 10; ++t) {
+      const int i = first + t;
+      red[w][i >> 3][sub * 8 + (i & 7)] = hs[t];
     }
-  if (lane < 8) {
-#pragma unroll
-    for (int j = 0; j < 5; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) red[w][j][sub * 8 + e] = acc[j][e];
   }
   __syncthreads();
 
