@@ -196,7 +196,7 @@ def test_vasc_c3_shape_two_layers():
 
 # ---------------------------------------------------------------- cdf threshold
 @pytest.mark.parametrize("K,Q,H,levels", [(7, 3, 2, None), (130, 65, 2, 4), (518, 20, 4, None), (2072, 6, 2, None),
-                                          (5000, 3, 2, 2), (8192, 2, 1, None)])
+                                          (4096, 4, 2, 3), (4096, 3, 1, None), (5000, 3, 2, 2), (8192, 2, 1, None)])
 def test_cdf_counts_bit_exact(K, Q, H, levels):
     """Per-row cdf counts and the capacity with the forced tail vs the oracle
     (scalar and per-head thresholds, the ratio lower bound, thresholds that

@@ -40,6 +40,8 @@
 
 #include "common.h"
 
+#include <rocprim/block/block_radix_sort.hpp>
+
 namespace vasc {
 namespace {
 
@@ -109,6 +111,40 @@ __device__ __forceinline__ float key_value(uint32_t key) {
   return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
+// The cdf count of one row from its keys sorted descending in LDS (a
+// multiple of 64 of them): the length of the longest prefix whose strictly
+// sequential float32 running sum stays <= T. The running sum is one chain
+// of adds (the prefix sums fl(S + x) of the sorted values, 64 per batch of
+// 16 LDS reads in flight); whether the prefix still holds is a second
+// chain beside it (a prefix that once exceeds T ends, whatever follows).
+// The LDS offset goes through an opaque VGPR: otherwise the compiler treats
+// the single walking lane's values as uniform and moves them through SGPRs
+// (readfirstlane and scalar ops between the adds, slower than the chain).
+__device__ __forceinline__ int cdf_walk(const uint4 *k4, int K, float T) {
+  float acc = 0.f;
+  int n = 0;
+  bool go = true;
+  int z = 0;
+  asm volatile("" : "+v"(z));
+  for (int b = 0; go && 64 * b < K; ++b) {
+    uint4 q[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) q[j] = k4[16 * b + j + z];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t kq[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // a padding key (0, past the row end) reads as NaN and ends the prefix
+        acc = acc + key_value(kq[e]);
+        go = go && acc <= T;
+        n += go ? 1 : 0;
+      }
+    }
+  }
+  return n;
+}
+
 __global__ __launch_bounds__(256) void cdf_count_kernel(const float *score, int64_t H, int64_t Q, int K, int n2,
                                                         const float *thr, int32_t min_count, int32_t force_last,
                                                         int32_t *count_out, int32_t *base_out) {
@@ -143,31 +179,99 @@ __global__ __launch_bounds__(256) void cdf_count_kernel(const float *score, int6
   }
   __syncthreads();
   if (tid == 0) {
-    const float T = thr[(row / Q) % H];
-    // 64 sorted keys per batch (16 LDS reads in flight; n2 is a multiple of
-    // 64); the running sum is the only serial chain.
-    const uint4 *k4 = reinterpret_cast<const uint4 *>(ckeys);
-    float acc = 0.f;
-    int n = 0;
-    bool go = true;
-    for (int b = 0; go && 64 * b < K; ++b) {
-      uint4 q[16];
+    int n = cdf_walk(reinterpret_cast<const uint4 *>(ckeys), K, thr[(row / Q) % H]);
+    n = n > min_count ? n : min_count;
+    n = n == 0 ? 1 : (n > K ? K : n);
+    count_out[row] = n;
+    if (base_out) base_out[row] = n + ((force_last && n < K && sbeat >= n) ? 1 : 0);
+  }
+}
+
+// The same count with the row sorted by rocPRIM's LDS block radix sort (256
+// threads, kItems keys each; 8-bit digits, four passes over 32-bit keys)
+// instead of the bitonic network, which costs O(K log^2 K) compare-exchanges
+// with a barrier per stage. Keys load lane-strided (coalesced), padding keys
+// 0 sort last; after the descending sort thread t holds ranks
+// [kItems t, kItems t + kItems), which it writes back to LDS for the same
+// sequential walk.
+template <int kItems>
+__global__ __launch_bounds__(256) void cdf_count_radix_kernel(const float *score, int64_t H, int64_t Q, int K,
+                                                              const float *thr, int32_t min_count,
+                                                              int32_t force_last, int32_t *count_out,
+                                                              int32_t *base_out) {
+  using Sort = rocprim::block_radix_sort<uint32_t, 256, kItems>;
+  __shared__ union {
+    typename Sort::storage_type sort;
+    float4 vals4[64 * kItems];  // the sorted values, then their prefix sums
+  } sm;
+  __shared__ int sbeat, sfail, swalked;
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float *srow = score + row * K;
+  const uint32_t last = order_key(srow[K - 1]);
+  if (tid == 0) {
+    sbeat = 0;
+    sfail = K;
+  }
+  uint32_t key[kItems];
+  int beat = 0;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) q[j] = k4[16 * b + j];
+  for (int i = 0; i < kItems; ++i) {
+    const int k = tid + 256 * i;
+    key[i] = k < K ? order_key(srow[k]) : 0u;
+    beat += k < K - 1 && key[i] >= last;
+  }
+  __syncthreads();
+  if (force_last && base_out) atomicAdd(&sbeat, beat);
+  Sort().sort_desc(key, sm.sort);
+  __syncthreads();  // the sort's storage is reused for the sorted values
+  float *vals = reinterpret_cast<float *>(sm.vals4);
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) vals[kItems * tid + i] = key_value(key[i]);  // padding: NaN
+  __syncthreads();
+  const float T = thr[(row / Q) % H];
+  if (tid == 0) {
+    // the running sum alone is serial: prefix sums written in place, 64 per
+    // batch (16 LDS reads in flight), until a batch ends above T (or NaN)
+    int z = 0;
+    asm volatile("" : "+v"(z));  // keeps the walk in VGPRs (see cdf_walk)
+    float acc = 0.f;
+    int b = 0;
+    for (; 64 * b < K; ++b) {
+      float4 q[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) q[j] = sm.vals4[16 * b + j + z];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const uint32_t kq[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+        acc += q[j].x;
+        q[j].x = acc;
+        acc += q[j].y;
+        q[j].y = acc;
+        acc += q[j].z;
+        q[j].z = acc;
+        acc += q[j].w;
+        q[j].w = acc;
+      }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 64 * b + 4 * j + e;
-          const float next = acc + key_value(kq[e]);
-          const bool ok = go && i < K && next <= T;
-          n = ok ? i + 1 : n;
-          acc = ok ? next : acc;
-          go = ok;
-        }
+      for (int j = 0; j < 16; ++j) sm.vals4[16 * b + j + z] = q[j];
+      if (!(acc <= T)) {
+        ++b;
+        break;
       }
     }
+    swalked = 64 * b;
+  }
+  __syncthreads();
+  // the prefix ends at the first sum that is not <= T (every later one is
+  // past the prefix whatever its value)
+  const int walked = swalked;
+  int fail = K;
+  for (int i = tid; i < walked; i += 256)
+    if (!(vals[i] <= T)) fail = i < fail ? i : fail;
+  if (fail < K) atomicMin(&sfail, fail);
+  __syncthreads();
+  if (tid == 0) {
+    int n = sfail;
     n = n > min_count ? n : min_count;
     n = n == 0 ? 1 : (n > K ? K : n);
     count_out[row] = n;
@@ -1931,10 +2035,23 @@ extern "C" int vasc_cdf_counts(const float *score, int64_t B, int64_t H, int64_t
   VASC_SUPPORTED(K <= 8192, "K=%lld key blocks not built (built: <= 8192)", (long long)K);
   VASC_REQUIRE(min_count >= 0 && min_count <= K, "min_count %d outside [0, K]", min_count);
   VASC_REQUIRE(B * H * Q < (int64_t(1) << 31), "too many rows");
+  const dim3 grid(static_cast<unsigned>(B * H * Q));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int Ki = static_cast<int>(K);
+  if (K <= 256 * 16) {
+    // rows of up to 4096 key blocks: the radix-sorted count
+    auto kern = K <= 256 ? cdf_count_radix_kernel<1>
+                : K <= 512 ? cdf_count_radix_kernel<2>
+                : K <= 1024 ? cdf_count_radix_kernel<4>
+                : K <= 2048 ? cdf_count_radix_kernel<8>
+                : cdf_count_radix_kernel<16>;
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, score, H, Q, Ki, thresholds, min_count, force_last, count_out,
+                       base_out);
+    return check_launch("vasc_cdf_counts");
+  }
   int n2 = 64;
   while (n2 < K) n2 <<= 1;
-  hipLaunchKernelGGL(cdf_count_kernel, dim3(static_cast<unsigned>(B * H * Q)), dim3(256),
-                     static_cast<size_t>(n2) * 4, reinterpret_cast<hipStream_t>(stream), score, H, Q,
-                     static_cast<int>(K), n2, thresholds, min_count, force_last, count_out, base_out);
+  hipLaunchKernelGGL(cdf_count_kernel, grid, dim3(256), static_cast<size_t>(n2) * 4, st, score, H, Q, Ki, n2,
+                     thresholds, min_count, force_last, count_out, base_out);
   return check_launch("vasc_cdf_counts");
 }
