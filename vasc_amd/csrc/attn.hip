@@ -371,13 +371,20 @@ void bsattn_fwd_kernel(const AttnParams p) {
       if (!dense) {
         const int lim = valid_keys(cur);
         float mx = -5000000.0f;
+        if (lim == kBlockK) {  // a whole block (the usual case): no per-key masks
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+          for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kk = 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
-            mx = kk < lim ? fmaxf(mx, S[t][r]) : mx;
-          }
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[t][r]);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int kk = 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
+              mx = kk < lim ? fmaxf(mx, S[t][r]) : mx;
+            }
+        }
         mx = fmaxf(mx, xor_lane(mx, 32)) * c;
         float gap = mx - run_max;  // the wave's largest, by VALU cross-lane moves (rows 0-31, both halves)
 #pragma unroll
