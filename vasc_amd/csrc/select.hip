@@ -438,14 +438,16 @@ __global__ __launch_bounds__(1024) void arrival_kernel(const SelectParams p, int
 // capacity and admitted debt. Wave 0 of every workgroup recomputes the head's
 // debt sum and pair capacity (canonical wave sums); workgroup 0 of the head
 // also publishes the head's partials of the three global gate sums.
-__global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
+// Waves 0-3 take 256 pairs each workgroup; wave 4 computes the head's sums
+// beside them (both are chains of dependent global loads, which now overlap).
+__global__ __launch_bounds__(320) void head_kernel(const SelectParams p) {
   __shared__ float sh_pc, sh_dsum;
   const int64_t bh = blockIdx.y;
   const int tid = threadIdx.x;
   // this thread's pair: its chunk partials and ledger inputs do not depend on
   // the per-head sums below, so they load before the barrier
   const int64_t pp = static_cast<int64_t>(blockIdx.x) * 256 + tid;
-  const bool has = pp < p.P;
+  const bool has = tid < 256 && pp < p.P;
   double acc_pp = 0.0;
   float refl_pp = 0.f, sig_pp = 0.f, d_pp = 0.f;
   if (has) {
@@ -455,14 +457,15 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
     for (int64_t c = 0; c < p.nchunks; ++c) acc_pp = acc_pp + part[c * p.P];
     d_pp = settle_one(p, bh * p.P + pp, &refl_pp, &sig_pp);
   }
-  if (tid < 64) {
+  if (tid >= 256) {
+    const int lane = tid - 256;
     double acc = 0.0, dacc = 0.0, useful = 0.0, wasted = 0.0, consumed = 0.0;
     // unrolled so several iterations' loads are in flight; the float64 chains
     // keep their order
 #pragma unroll 16
-    for (int64_t q = tid; q < p.Q; q += 64) acc = acc + static_cast<double>(p.rowpair[bh * p.Q + q]);
+    for (int64_t q = lane; q < p.Q; q += 64) acc = acc + static_cast<double>(p.rowpair[bh * p.Q + q]);
 #pragma unroll 8
-    for (int64_t j = tid; j < p.P; j += 64) {
+    for (int64_t j = lane; j < p.P; j += 64) {
       float refl, sig;
       const float d = settle_one(p, bh * p.P + j, &refl, &sig);
       dacc = dacc + static_cast<double>(d);
@@ -475,7 +478,7 @@ __global__ __launch_bounds__(256) void head_kernel(const SelectParams p) {
     useful = wave_butterfly(useful);
     wasted = wave_butterfly(wasted);
     consumed = wave_butterfly(consumed);
-    if (tid == 0) {
+    if (lane == 0) {
       sh_pc = static_cast<float>(s / static_cast<double>(p.Q));
       sh_dsum = static_cast<float>(ds);
       if (blockIdx.x == 0) {
@@ -1808,7 +1811,7 @@ int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
     }
     if ((rc = check_launch("vasc_select_blocks/arrival"))) return rc;
     hipLaunchKernelGGL(head_kernel, dim3(static_cast<unsigned>(cdiv(p.P, 256)), static_cast<unsigned>(p.BH)),
-                       dim3(256), 0, s, p);
+                       dim3(320), 0, s, p);
     if ((rc = check_launch("vasc_select_blocks/head"))) return rc;
   }
   if ((rc = launch_select(p, vasc, s))) return rc;
