@@ -248,6 +248,29 @@ int vasc_cdf_counts(const float *score, int64_t B, int64_t H, int64_t Q,
                     int32_t force_last, int32_t *count_out, int32_t *base_out,
                     void *stream);
 
+/*
+ * The VASC selector's selected indices: per row, the M blocks of largest
+ * priority, largest first, equal priorities in ascending block index.
+ * Replaces priority.topk(M, dim=-1, sorted=True).indices
+ * (sparse_wrapper.py:3887-3894), stored as routing_state
+ * "cosa_value_risk_pair_selected_indices" (sparse_wrapper.py:4024-4026).
+ *
+ * priority   [rows,K] float32 contiguous (vasc_select_blocks' priority_out).
+ * index      optional [rows,width] int32: vasc_select_blocks' index lists
+ *            of a selection that kept each row's largest priorities under
+ *            the same tie rule (the VASC selection that wrote `priority`;
+ *            count: their counts, sink: the sink blocks appended to each
+ *            list). A row that kept exactly M patch blocks takes them from
+ *            its list instead of ranking the row.
+ * order_out  [rows,M] int64.
+ * 0 <= M <= K (M == 0 writes nothing); width >= M + sink when index is
+ * given. Built variant: K <= 8192.
+ */
+int vasc_priority_order(const float *priority, const int32_t *index,
+                        const int32_t *count, int64_t width, int32_t sink,
+                        int64_t rows, int64_t K, int64_t M, int64_t *order_out,
+                        void *stream);
+
 /* Elements (bf16) of the packed V buffer for these sizes. */
 int64_t vasc_packed_v_elems(int64_t B, int64_t H, int64_t nk, int64_t d);
 

@@ -18,6 +18,8 @@ Follows ``src/sparse_vggt/utils/sparse_wrapper.py`` (``SW``) of the reference:
                            projection (``SW:1755-1769``), QK-admission service
                            reduced from the selected indices
                            (``SW:2922-2980``).
+* ``selected_indices``     the selector's ``priority.topk(M, sorted=True)``
+                           indices (``SW:3887-3894``).
 * ``finalize``             ``finalize_cosa_value_risk_pair_debt``
                            (``SW:4101-4177``).
 
@@ -35,7 +37,8 @@ finite priority, memory activates, terminal settlement idempotent) and closed
 forms: layer 0 priority equals the conservative arrival, uniform innovation
 without saturation reduces to Top-K on the score, zero innovation selects the
 first ``cap`` indices, zero debt disables the gate, brute-force Top-K on tiny
-rows. The cdf count is pinned against torch's own sort / cumsum /
+rows; the selected indices against torch's own topk on rows of distinct
+priorities and a brute-force sort with ties. The cdf count is pinned against torch's own sort / cumsum /
 searchsorted (the reference's primitives) on dyadic scores, where every
 prefix sum is exact, and against a brute-force loop and closed forms.
 """
@@ -56,6 +59,27 @@ SERVICE_KEY = "qk_pv_service_observation"
 # --------------------------------------------------------------------------
 # Top-c selection with the canonical tie rule
 # --------------------------------------------------------------------------
+def priority_order(priority: np.ndarray) -> np.ndarray:
+    """Each row's indices, largest priority first, ties in ascending index.
+
+    Canonical form of ``priority.topk(K, sorted=True).indices``; int64.
+    """
+    prio = np.asarray(priority, dtype=np.float32)
+    K = prio.shape[-1]
+    key = order_key(prio).astype(np.uint64)
+    idx = np.arange(K, dtype=np.uint64)
+    composite = (key << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)
+    return np.argsort(composite, axis=-1, kind="stable")[..., ::-1].astype(np.int64)
+
+
+def selected_indices(priority: np.ndarray, M: int) -> np.ndarray:
+    """The selector's ``selected_indices`` (SW:3887-3894, stored at
+    SW:4024-4026): ``priority.topk(M, dim=-1, sorted=True).indices``, the M
+    largest priorities of each row in descending order, ties in ascending
+    index. int64 ``[..., M]``."""
+    return priority_order(priority)[..., :int(M)]
+
+
 def select_top(priority: np.ndarray, count: np.ndarray) -> np.ndarray:
     """Boolean mask of the ``count[...]`` largest entries of each row.
 
@@ -64,10 +88,7 @@ def select_top(priority: np.ndarray, count: np.ndarray) -> np.ndarray:
     """
     prio = np.asarray(priority, dtype=np.float32)
     K = prio.shape[-1]
-    key = order_key(prio).astype(np.uint64)
-    idx = np.arange(K, dtype=np.uint64)
-    composite = (key << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)
-    order = np.argsort(composite, axis=-1, kind="stable")[..., ::-1]
+    order = priority_order(prio)
     rank = np.empty_like(order)
     np.put_along_axis(rank, order, np.broadcast_to(np.arange(K), order.shape), axis=-1)
     c = np.clip(np.broadcast_to(np.asarray(count), prio.shape[:-1]), 0, K)
@@ -378,6 +399,7 @@ def cosa_select(score, pooled_value, cap, *, layer_idx: int, state: dict,
     }
     state["cosa_value_risk_pair_priority"] = prio
     state["cosa_value_risk_pair_max_patch_blocks"] = int(M)
+    state["cosa_value_risk_pair_selected_indices"] = selected_indices(prio, M)
     state["cosa_value_risk_pair_qk_order_priority"] = s
     info = dict(arrival=arrival, pair_cap=pair_cap, row_arrival=A, row_pair=a,
                 rowpair=rowpair, total=total, gate=gate, admitted=adm,

@@ -143,6 +143,8 @@ def test_cosa_mask_api_chain_bit_exact(release_env):
         assert np.array_equal(_bits(st_gpu[SW.STATE_KEY]), np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
         assert np.array_equal(_bits(st_gpu[SW.PENDING_KEY]), st_ref[OS.PENDING_KEY].view(np.uint32))
         assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_priority"]), info["priority"].view(np.uint32))
+        assert np.array_equal(st_gpu["cosa_value_risk_pair_selected_indices"].cpu().numpy(),
+                              st_ref["cosa_value_risk_pair_selected_indices"])
         assert np.array_equal(st_gpu["cosa_value_risk_pair_qk_order_priority"].cpu().numpy(),
                               np.asarray(st_ref["cosa_value_risk_pair_qk_order_priority"], np.float32))
     t_gpu = SW.finalize_cosa_value_risk_pair_debt(st_gpu)
@@ -191,21 +193,26 @@ def test_block_sparse_attn_c1_end_to_end(release_env, model):
         assert np.array_equal(_bits(st_gpu["cosa_value_risk_pair_debt"]),
                               np.asarray(st_ref[OS.STATE_KEY], np.float32).view(np.uint32))
         kb = -(-Np // 64)
-        _check_selected_indices(st_gpu, final, kb, int(kb * 0.25) + int(model == "pi3"))
+        _check_selected_indices(st_gpu, st_ref, final, kb, int(kb * 0.25) + int(model == "pi3"))
 
 
-def _check_selected_indices(state, final, kb, M):
-    """routing_state's selected indices: width M (the capacity hint, as the
-    reference's ``max_patch_blocks``), each row's kept patch blocks ascending,
-    then the sink block ids kb.., then -1."""
+def _check_selected_indices(state, ref_state, final, kb, M):
+    """routing_state's execution priority and selected indices: width M (the
+    capacity hint, as the reference's ``max_patch_blocks``), the M largest
+    priorities of each row in descending order (``priority.topk(M,
+    sorted=True)``, int64), bit-exact with the oracle; the first ``count``
+    of them are the row's kept patch blocks."""
+    assert np.array_equal(_bits(state["cosa_value_risk_pair_priority"]),
+                          np.asarray(ref_state["cosa_value_risk_pair_priority"], np.float32).view(np.uint32))
     got = state["cosa_value_risk_pair_selected_indices"].cpu().numpy()
     assert state["cosa_value_risk_pair_max_patch_blocks"] == M and got.shape == final.shape[:-1] + (M,)
-    sink = final.shape[-1] - kb
-    rows_final = final.reshape(-1, final.shape[-1])
-    for r, row in enumerate(got.reshape(-1, M)):
-        kept = np.flatnonzero(rows_final[r, :kb])
-        expect = np.concatenate([kept, kb + np.arange(sink), np.full(M, -1)])[:M]
-        assert np.array_equal(row, expect), r
+    assert got.dtype == np.int64
+    assert np.array_equal(got, ref_state["cosa_value_risk_pair_selected_indices"])
+    kept = final[..., :kb]
+    cnt = kept.sum(-1)
+    rows_got, rows_kept = got.reshape(-1, M), kept.reshape(-1, kb)
+    for r, c in enumerate(cnt.reshape(-1)):
+        assert np.array_equal(np.sort(rows_got[r, :c]), np.flatnonzero(rows_kept[r])), r
 
 
 @pytest.mark.parametrize("model,mode", [("pi3", "topk"), ("pi3", "vasc"), ("vggt", "vasc")])

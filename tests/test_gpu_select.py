@@ -142,6 +142,11 @@ def _run_chain(K, Q, H, layers, *, topk, force_last, sink, peak, seed, row_caps=
         assert gate == int(info["gate"]), f"layer {layer}: gate {gate} != {info['gate']}"
         gates.append(gate)
         assert np.array_equal(_bits(out["priority"].cpu()), _bits(info["priority"])), f"layer {layer}: priority"
+        expect = OS.selected_indices(info["priority"], info["M"])
+        order = ops.priority_order(out["priority"], M).cpu().numpy()
+        assert np.array_equal(order, expect), f"layer {layer}: order"
+        order = ops.priority_order(out["priority"], M, out["index"], out["count"], sink).cpu().numpy()
+        assert np.array_equal(order, expect), f"layer {layer}: order from the lists"
         assert np.array_equal(out["mask"].cpu().numpy().astype(bool), sel), f"layer {layer}: support"
         _assert_lists(out, sel, sink)
         for key in ("debt", "arrival", "service"):
@@ -192,6 +197,52 @@ def test_vasc_c4_shape_two_layers():
 def test_vasc_c3_shape_two_layers():
     """Config 3 shape: H=16, 1036 x 2072 blocks at s=0.875 structural (224 blocks)."""
     _run_chain(2072, 1036, 16, 2, topk=224, force_last=False, sink=10, peak=2.0, seed=3)
+
+
+@pytest.mark.parametrize("K", [1, 2, 7, 130, 257, 518, 1036, 2072, 2113, 4096, 5000, 8192])
+def test_priority_order_bit_exact(K):
+    """The selected indices (priority.topk(M, sorted=True)): every M from 1 to
+    K on rows of distinct priorities, exact ties (few levels), zeros,
+    protected FLT_MAX blocks and constant rows; equal priorities in
+    ascending block index."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(K)
+    rows = []
+    rows.append(rng.random(K).astype(np.float32))
+    rows.append(rng.integers(0, 4, K).astype(np.float32) / np.float32(3))   # ties
+    r = rng.random(K).astype(np.float32)
+    r[rng.random(K) < 0.5] = 0.0                                            # zeros
+    rows.append(r)
+    r = rng.random(K).astype(np.float32) + np.float32(1.0)
+    r[rng.random(K) < 0.05] = np.float32(3.4028235e38)                      # protected
+    rows.append(r)
+    rows.append(np.full(K, 0.25, np.float32))                              # constant
+    rows.append((rng.random(K) * 2.0 ** rng.integers(-60, 60, K)).astype(np.float32))  # wide exponent range
+    prio = np.stack(rows).reshape(2, 3, 1, K)
+    g = torch.from_numpy(prio).cuda()
+    for M in sorted(m for m in {1, 2, K // 7, K // 4, K // 2, K - 1, K} if 1 <= m <= K):
+        got = ops.priority_order(g, M).cpu().numpy()
+        assert got.shape == (2, 3, 1, M) and got.dtype == np.int64
+        assert np.array_equal(got, OS.selected_indices(prio, M)), f"K={K} M={M}"
+    assert ops.priority_order(g, 0).shape == (2, 3, 1, 0)
+
+
+@pytest.mark.parametrize("K,M", [(130, 33), (518, 120), (518, 155), (1036, 310), (2072, 224), (2072, 700),
+                                 (4096, 1024), (8192, 2048)])
+def test_priority_order_from_select_lists(K, M):
+    """Rows that kept exactly M blocks take them from the select pass's lists
+    (after their sink entries are discounted), the others rank their row; a
+    launch mixes both."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(K + M)
+    score = _scores(rng, (1, 2, 9, K), levels=8)
+    cap = np.where(rng.random((1, 2, 9)) < 0.5, M, max(M - 3, 1)).astype(np.int32)
+    g = torch.from_numpy(score).cuda()
+    sel = ops.select_blocks(g, mode=TOPK, topk=0, row_cap=torch.from_numpy(cap).cuda(), max_capacity=M,
+                            sink_blocks=2)
+    assert np.array_equal(sel["count"].cpu().numpy(), cap + 2)
+    got = ops.priority_order(g, M, sel["index"], sel["count"], 2).cpu().numpy()
+    assert np.array_equal(got, OS.selected_indices(score, M))
 
 
 # ---------------------------------------------------------------- cdf threshold

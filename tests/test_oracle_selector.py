@@ -32,6 +32,38 @@ def test_select_top_matches_brute_force_with_lower_index_ties():
                 assert np.array_equal(got, expect), (prio, c)
 
 
+def test_selected_indices_match_torch_topk_on_distinct_priorities():
+    """The selector's selected_indices are ``priority.topk(M, sorted=True)``
+    (SW:3887-3894); on rows without ties torch's own topk fixes every entry,
+    including the order."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(11)
+    for K in (1, 2, 7, 130, 518, 2072):
+        prio = rng.permutation(np.arange(4 * K, dtype=np.float32))[:K] / np.float32(7)
+        prio = np.stack([prio, rng.permutation(prio), np.float32(3) - prio])
+        for M in sorted({0, 1, K // 4, K // 2 + 1, K}):
+            got = OS.selected_indices(prio, M)
+            expect = torch.from_numpy(prio).topk(M, dim=-1, sorted=True).indices.numpy()
+            assert got.dtype == np.int64 and got.shape == (3, M)
+            assert np.array_equal(got, expect), (K, M)
+
+
+def test_selected_indices_brute_force_with_ties():
+    """Descending priority, equal priorities in ascending index (the tie rule
+    of the selection); the first c entries are the selected set."""
+    rng = np.random.default_rng(12)
+    for K in range(1, 9):
+        for _ in range(40):
+            prio = rng.integers(0, 3, K).astype(np.float32)
+            prio[rng.random(K) < 0.1] = np.float32(3.4028235e38)  # protected blocks
+            full = OS.selected_indices(prio, K)
+            assert full.tolist() == sorted(range(K), key=lambda k: (-float(prio[k]), k))
+            for c in range(K + 1):
+                sel = np.zeros(K, bool)
+                sel[full[:c]] = True
+                assert np.array_equal(sel, OS.select_top(prio, np.array(c)))
+
+
 def test_check_selector_invariants():
     """tests/check_selector.py:44-65 of the reference, on the oracle."""
     rng = np.random.default_rng(20260906)

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
                                              P, P, P, P, P, P, P, P, P, P, I64, P, P]),
     "vasc_settle_terminal": (c_int32, [P, P, P, I64, P, P]),
     "vasc_cdf_counts": (c_int32, [P, I64, I64, I64, I64, P, I32, I32, P, P, P]),
+    "vasc_priority_order": (c_int32, [P, P, P, I64, I32, I64, I64, I64, P, P]),
     "vasc_packed_v_elems": (c_int64, [I64, I64, I64, I64]),
     "vasc_pack_v": (c_int32, [P, I64, I64, I64, I64, I64, I64, I64, P, P]),
     "vasc_block_sparse_attn_fwd": (c_int32, [P, I64, I64, I64, P, I64, I64, I64, P, P, I64, I64, I64,

@@ -1652,6 +1652,231 @@ void select_rows_kernel(const SelectParams p, int rows_per_wave) {
   }
 }
 
+// ------------------------------------------------------------------ order
+// The selector's priority order: per row the M largest priorities, largest
+// first, equal priorities in ascending block index (the selected indices,
+// priority.topk(M, sorted=True).indices). One wave per row. The M blocks come
+// from the select pass's index list when the row kept exactly M patch blocks
+// (its kept set is the top M under the same tie rule); otherwise the row's
+// order keys go to registers (k = lane + 64 m, padding 0), rows_threshold
+// finds the M-th largest key and the M blocks go to LDS in ascending index
+// order. Up to 1024 blocks are then sorted in registers (a bitonic network
+// over 64-bit composites key << 32 | ~block, descending, so equal keys end in
+// ascending block order); more take a stable LSD radix sort in LDS over the
+// key bytes that differ among them (descending digits; stability keeps equal
+// keys in ascending block order). Per wave, after the rank buffers: the
+// (key, block) buffers of M rounded up to 64 entries (two for the radix sort).
+
+// One stable pass over n (key, block) pairs from (sk, sv) to (dk, dv),
+// descending in the key byte at `shift`. `hist`: 256 words of this wave.
+__device__ void order_pass(const uint32_t *sk, const uint32_t *sv, uint32_t *dk, uint32_t *dv, int n, int shift,
+                           uint32_t *hist, int lane) {
+  *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
+  wave_sync();
+  for (int i = lane; i < n; i += 64) atomicAdd(&hist[255u - ((sk[i] >> shift) & 255u)], 1u);
+  wave_sync();
+  // exclusive prefix of the digit counts: four bins per lane, then across lanes
+  const u32x4 h = *reinterpret_cast<const u32x4 *>(hist + 4 * lane);
+  const int own = static_cast<int>(h[0] + h[1] + h[2] + h[3]);
+  int inc = own;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o);
+    if (lane >= o) inc += t;
+  }
+  const uint32_t e = static_cast<uint32_t>(inc - own);
+  *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{e, e + h[0], e + h[0] + h[1], e + h[0] + h[1] + h[2]};
+  wave_sync();
+  const uint64_t lt = lanemask_lt();
+  for (int b0 = 0; b0 < n; b0 += 64) {
+    const int i = b0 + lane;
+    const bool valid = i < n;
+    const uint32_t kk = valid ? sk[i] : 0u, vv = valid ? sv[i] : 0u;
+    const uint32_t d = 255u - ((kk >> shift) & 255u);
+    // the valid lanes holding the same digit
+    uint64_t same = __builtin_amdgcn_ballot_w64(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t bb = __builtin_amdgcn_ballot_w64(bit);
+      same &= bit ? bb : ~bb;
+    }
+    const uint32_t off = valid ? hist[d] : 0u;
+    wave_sync();  // every lane has read its digit's offset before the highest lane advances it
+    if (valid) {
+      const uint32_t at = off + static_cast<uint32_t>(__popcll(same & lt));
+      dk[at] = kk;
+      dv[at] = vv;
+      if ((same >> lane) == 1u) hist[d] = off + static_cast<uint32_t>(__popcll(same));
+    }
+    wave_sync();
+  }
+}
+
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v, int off) {
+  const uint64_t lo = xor_lane(static_cast<uint32_t>(v), off), hi = xor_lane(static_cast<uint32_t>(v >> 32), off);
+  return (hi << 32) | lo;
+}
+
+// Descending bitonic sort of 64 NPL composites, element e = NPL lane + j.
+// A merge step at STRIDE inside blocks of SIZE leaves the larger value at
+// the lower element of each pair in descending blocks ((e & SIZE) == 0),
+// the smaller in ascending ones. Levels and steps recurse at compile time.
+template <int NPL, int SIZE, int STRIDE>
+__device__ __forceinline__ void bitonic_step(uint64_t (&v)[NPL], int lane) {
+  if constexpr (STRIDE >= NPL) {
+    constexpr int lo = STRIDE / NPL;
+    const bool lower = (lane & lo) == 0;
+    const bool desc = (lane & (SIZE / NPL)) == 0;  // SIZE >= 2 NPL here
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const uint64_t o = xor_lane64(v[j], lo);
+      const bool big = v[j] > o;
+      v[j] = (lower == desc) == big ? v[j] : o;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      if (j & STRIDE) continue;
+      const bool desc = SIZE < NPL ? (j & SIZE) == 0 : (lane & (SIZE / NPL)) == 0;
+      const uint64_t a = v[j], b = v[j ^ STRIDE];
+      const bool swap = desc ? a < b : a > b;
+      v[j] = swap ? b : a;
+      v[j ^ STRIDE] = swap ? a : b;
+    }
+  }
+  if constexpr (STRIDE > 1) bitonic_step<NPL, SIZE, STRIDE / 2>(v, lane);
+}
+
+template <int NPL, int SIZE = 2>
+__device__ __forceinline__ void bitonic_desc(uint64_t (&v)[NPL], int lane) {
+  bitonic_step<NPL, SIZE, SIZE / 2>(v, lane);
+  if constexpr (SIZE < 64 * NPL) bitonic_desc<NPL, SIZE * 2>(v, lane);
+}
+
+__device__ __forceinline__ uint64_t order_composite(uint32_t key, uint32_t block) {
+  return (static_cast<uint64_t>(key) << 32) | static_cast<uint64_t>(0xffffffffu - block);
+}
+
+// NPL: sorted entries per lane (64 NPL >= M), 0 for the radix sort in LDS.
+// index / count / width / sink: the select pass's lists (index may be null).
+template <int EPT, int NPL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EPT <= 33 ? 4 : 1)))
+void order_rows_kernel(const float *prio, const int32_t *index, const int32_t *count, int64_t width, int sink,
+                       int64_t rows, int K, int M, int wave_words, int64_t *out) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  const int lane0 = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + w;
+  if (row >= rows) return;
+  uint32_t *hist = lds + static_cast<int64_t>(w) * wave_words;
+  uint32_t *sbuf = hist + 320;
+  uint32_t *cand = sbuf + 128;
+  const int Mp = (M + 63) & ~63;
+  uint32_t *k0 = cand + 64 * kSeg, *v0 = k0 + Mp;
+  const int lane = opaque_lane(lane0);
+  const float *prow = prio + row * K;
+  const int listed = index ? __builtin_amdgcn_readfirstlane(count[row] - sink) : -1;
+  constexpr int kRegs = NPL > 0 ? NPL : 1;
+  uint64_t v[kRegs];
+  if (NPL > 0 && listed == M) {
+    // the select pass's kept blocks (ascending; block ids clamped into the row)
+    const int32_t *irow = index + row * width;
+#pragma unroll
+    for (int j = 0; j < kRegs; ++j) {
+      const int e = NPL * lane + j;
+      int blk = e < M ? irow[e] : 0;
+      blk = blk < 0 ? 0 : (blk >= K ? K - 1 : blk);
+      v[j] = e < M ? order_composite(order_key(prow[blk]), static_cast<uint32_t>(blk)) : 0u;
+    }
+  } else {
+    if (listed == M) {
+      const int32_t *irow = index + row * width;
+      for (int i = lane; i < M; i += 64) {
+        int blk = irow[i];
+        blk = blk < 0 ? 0 : (blk >= K ? K - 1 : blk);
+        k0[i] = order_key(prow[blk]);
+        v0[i] = static_cast<uint32_t>(blk);
+      }
+    } else {
+      float x[EPT];
+      load_slots(x, prow, K, lane);
+      uint32_t key[EPT];
+#pragma unroll
+      for (int m = 0; m < EPT; ++m) key[m] = lane + 64 * m < K ? order_key(x[m]) : 0u;
+      // keys > T kept, keys == T in index order up to need (M >= 1: T is a real key)
+      uint32_t T = 0xffffffffu;
+      int need = 0, eqT = 1;
+      rows_threshold(key, lane, M, hist, sbuf, cand, T, need, eqT);
+      const bool split = need < eqT;
+      int base = 0, run_eq = 0;
+#pragma unroll
+      for (int m = 0; m < EPT; ++m) {
+        const uint32_t xk = key[m];
+        bool sel = xk >= T;
+        if (split) {
+          const bool eq = xk == T;
+          const uint64_t beq = __builtin_amdgcn_ballot_w64(eq);
+          sel = xk > T || (eq && run_eq + lanes_below(beq) < need);
+          run_eq += __popcll(beq);
+        }
+        const uint64_t bm = __builtin_amdgcn_ballot_w64(sel);
+        if (sel) {
+          const int at = base + lanes_below(bm);
+          k0[at] = xk;
+          v0[at] = static_cast<uint32_t>(lane + 64 * m);
+        }
+        base += __popcll(bm);
+      }
+    }
+    wave_sync();
+    if (NPL > 0) {
+#pragma unroll
+      for (int j = 0; j < kRegs; ++j) {
+        const int e = NPL * lane + j;
+        v[j] = e < M ? order_composite(k0[e], v0[e]) : 0u;
+      }
+    }
+  }
+  int64_t *orow = out + row * M;
+  if (NPL > 0) {
+    bitonic_desc<kRegs>(v, lane);
+#pragma unroll
+    for (int j = 0; j < kRegs; ++j) {
+      const int e = NPL * lane + j;
+      if (e < M) orow[e] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(v[j]));
+    }
+    return;
+  }
+  // radix: the kept keys lie in [min, max]; bytes above the highest bit where
+  // those differ are common to all of them and need no pass
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+  for (int i = lane; i < M; i += 64) {
+    kmin = k0[i] < kmin ? k0[i] : kmin;
+    kmax = k0[i] > kmax ? k0[i] : kmax;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t a = static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmin), o));
+    const uint32_t b = static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), o));
+    kmin = a < kmin ? a : kmin;
+    kmax = b > kmax ? b : kmax;
+  }
+  const uint32_t diff = __builtin_amdgcn_readfirstlane(kmax ^ kmin);
+  const int passes = diff ? (31 - __clz(static_cast<int>(diff))) / 8 + 1 : 0;
+  uint32_t *sk = k0, *sv = v0, *dk = v0 + Mp, *dv = v0 + 2 * Mp;
+  for (int ps = 0; ps < passes; ++ps) {
+    order_pass(sk, sv, dk, dv, M, 8 * ps, hist, lane);
+    uint32_t *t = sk;
+    sk = dk;
+    dk = t;
+    t = sv;
+    sv = dv;
+    dv = t;
+  }
+  for (int i = lane; i < M; i += 64) orow[i] = static_cast<int64_t>(sv[i]);
+}
+
 __global__ void settle_terminal_kernel(const float *debt_in, const float *pending, const float *service, int64_t n,
                                        float *out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -1753,6 +1978,64 @@ int launch_select_rows(const SelectParams &p, hipStream_t s) {
   if (K <= 2112 || !kVasc) return launch_select_rows_cfg<kVasc, 33>(p, s);
   if (K <= 3072) return launch_select_rows_cfg<kVasc, 48>(p, s);
   return launch_select_rows_cfg<kVasc, 64>(p, s);
+}
+
+// Priority order: as many row waves per workgroup (up to 4) as keep the
+// workgroup's LDS within 64 KB; a single wave takes more (up to 137 KB at
+// 8192 blocks).
+struct OrderArgs {
+  const float *prio;
+  const int32_t *index, *count;
+  int64_t width;
+  int sink;
+  int64_t rows;
+  int K, M;
+  int64_t *out;
+};
+
+template <int EPT, int NPL>
+int launch_order_cfg(const OrderArgs &a, hipStream_t s) {
+  const int wave_words = kRowWaveWords + (NPL > 0 ? 2 : 4) * ((a.M + 63) & ~63);
+  const size_t wave_bytes = static_cast<size_t>(wave_words) * 4;
+  int waves = static_cast<int>((64 * 1024) / wave_bytes);
+  waves = waves < 1 ? 1 : (waves > kWaves ? kWaves : waves);
+  const size_t lds_bytes = wave_bytes * waves;
+  const void *kern = reinterpret_cast<const void *>(order_rows_kernel<EPT, NPL>);
+  int rc;
+  if ((rc = reserve_lds(kern, lds_bytes))) return rc;
+  hipLaunchKernelGGL((order_rows_kernel<EPT, NPL>), dim3(static_cast<unsigned>(cdiv(a.rows, waves))),
+                     dim3(64 * waves), lds_bytes, s, a.prio, a.index, a.count, a.width, a.sink, a.rows, a.K, a.M,
+                     wave_words, a.out);
+  return check_launch("vasc_priority_order");
+}
+
+// Sorted entries per lane: the fewest that hold M (rows of K <= 64 EPT keys
+// hold M <= K); the radix sort past 1024.
+template <int EPT>
+int launch_order_npl(const OrderArgs &a, hipStream_t s) {
+  if (a.M <= 64) return launch_order_cfg<EPT, 1>(a, s);
+  if (a.M <= 128) return launch_order_cfg<EPT, 2>(a, s);
+  if constexpr (64 * EPT <= 256) {
+    return launch_order_cfg<EPT, 4>(a, s);
+  } else {
+    if (a.M <= 256) return launch_order_cfg<EPT, 4>(a, s);
+    if (a.M <= 512) return launch_order_cfg<EPT, 8>(a, s);
+    if constexpr (64 * EPT <= 1024) {
+      return launch_order_cfg<EPT, 16>(a, s);
+    } else {
+      if (a.M <= 1024) return launch_order_cfg<EPT, 16>(a, s);
+      return launch_order_cfg<EPT, 0>(a, s);
+    }
+  }
+}
+
+int launch_order(const OrderArgs &a, hipStream_t s) {
+  if (a.K <= 256) return launch_order_npl<4>(a, s);
+  if (a.K <= 576) return launch_order_npl<9>(a, s);
+  if (a.K <= 1088) return launch_order_npl<17>(a, s);
+  if (a.K <= 2112) return launch_order_npl<33>(a, s);
+  if (a.K <= 4096) return launch_order_npl<64>(a, s);
+  return launch_order_npl<128>(a, s);
 }
 
 // Register rows serve VASC up to 4096 key blocks (after the register-row
@@ -2057,4 +2340,22 @@ extern "C" int vasc_cdf_counts(const float *score, int64_t B, int64_t H, int64_t
   hipLaunchKernelGGL(cdf_count_kernel, grid, dim3(256), static_cast<size_t>(n2) * 4, st, score, H, Q, Ki, n2,
                      thresholds, min_count, force_last, count_out, base_out);
   return check_launch("vasc_cdf_counts");
+}
+
+extern "C" int vasc_priority_order(const float *priority, const int32_t *index, const int32_t *count, int64_t width,
+                                   int32_t sink, int64_t rows, int64_t K, int64_t M, int64_t *order_out,
+                                   void *stream) {
+  using namespace vasc;
+  VASC_REQUIRE(priority && order_out, "priority and order_out are required");
+  VASC_REQUIRE(!index || count, "index needs count");
+  VASC_REQUIRE(rows > 0 && K > 0, "sizes must be positive");
+  VASC_SUPPORTED(K <= 8192, "K=%lld key blocks not built (built: <= 8192)", (long long)K);
+  VASC_REQUIRE(M >= 0 && M <= K, "M=%lld outside [0, K]", (long long)M);
+  VASC_REQUIRE(!index || (sink >= 0 && width >= M + sink), "index rows of width %lld cannot hold M + sink entries",
+               (long long)width);
+  VASC_REQUIRE(rows < (int64_t(1) << 31), "too many rows");
+  if (M == 0) return VASC_OK;
+  const OrderArgs a{priority, index, index ? count : nullptr, width, sink, rows, static_cast<int>(K),
+                    static_cast<int>(M), order_out};
+  return launch_order(a, reinterpret_cast<hipStream_t>(stream));
 }

@@ -226,6 +226,36 @@ def cdf_counts(score: torch.Tensor, cdf_threshold, *, min_count: int = 0, force_
     return count, base
 
 
+def priority_order(priority: torch.Tensor, M: int, index: torch.Tensor | None = None,
+                   count: torch.Tensor | None = None, sink: int = 0) -> torch.Tensor:
+    """The selector's selected indices (kernel 2): per row the ``M`` blocks
+    of largest priority, largest first, equal priorities in ascending block
+    index, as ``priority.topk(M, dim=-1, sorted=True).indices``
+    (SW:3887-3894). ``priority`` float32 ``[..., K]``; returns int64
+    ``[..., M]``. ``index`` / ``count`` / ``sink``: the ``select_blocks``
+    lists of the same selection; rows that kept exactly ``M`` patch blocks
+    take them from there."""
+    _dev(priority, "priority")
+    p = priority.float().contiguous()
+    K = p.shape[-1]
+    if not 0 <= int(M) <= K:
+        raise ValueError(f"M={M} outside [0, {K}]")
+    out = torch.empty(p.shape[:-1] + (int(M),), device=p.device, dtype=torch.int64)
+    rows = p.numel() // K if K else 0
+    width = 0
+    if index is not None:
+        if count is None or index.dtype != torch.int32 or count.dtype != torch.int32:
+            raise ValueError("index and count must be the int32 lists of select_blocks")
+        if index.shape[:-1] != p.shape[:-1] or count.shape != p.shape[:-1]:
+            raise ValueError("index and count must match the priority rows")
+        index, count = index.contiguous(), count.contiguous()
+        width = index.shape[-1]
+    if rows and M:
+        _lib.call("vasc_priority_order", p.data_ptr(), _ptr(index), _ptr(count), width, int(sink), rows, K, int(M),
+                  out.data_ptr(), _stream())
+    return out
+
+
 def settle_terminal(debt, pending_arrival, service) -> torch.Tensor:
     pend = pending_arrival.float().contiguous()
     svc = service.float().contiguous()

@@ -16,16 +16,13 @@ Mirrors the operator surface of the reference's
 Every function runs the HIP kernels of ``libvasc_hip.so``; CPU tensors are
 rejected. Documented differences from the reference: attention computes in
 bf16 with fp32 accumulation (the reference quantises Q/K to int8 and P to
-fp16); ``routing_state["cosa_value_risk_pair_selected_indices"]`` ([B,H,Q,M]
-int32) holds each row's kept patch blocks in ascending order, then the sink
-block ids K.. and -1 to width M (the reference stores ``priority.topk(M)``
-indices in descending priority, SW:3890-3894); M
-(``cosa_value_risk_pair_max_patch_blocks``) is the capacity hint with a
+fp16); M (``cosa_value_risk_pair_max_patch_blocks``) is the capacity hint with a
 ratio, as in the reference, and ``max(topk, 1) + force_last`` with an
 explicit ``topk`` where the reference reads the largest row capacity back to
 the host (equal unless every row already keeps the mixed-tail block); ties in
-the selection go to the lower block index (``torch.topk`` leaves them
-unspecified).
+the selection and in ``routing_state["cosa_value_risk_pair_selected_indices"]``
+(``priority.topk(M, sorted=True).indices``, int64) go to the lower block
+index (``torch.topk`` leaves them unspecified).
 """
 from __future__ import annotations
 
@@ -169,11 +166,13 @@ def _service_domain() -> str:
 
 
 def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_idx: int, M: int,
-                    domain: str = "qk_admission", priority: torch.Tensor | None = None) -> None:
+                    domain: str = "qk_admission", priority: torch.Tensor | None = None, sink: int = 0) -> None:
     """State writes of the selector (SW:3990-4025). In the QK-admission domain
     the service observation is recorded here; in the PV-execution domain the
-    attention launch records it (``_record_pv_execution``). ``priority``: the
-    cleaned score when the pooled softmax already wrote it."""
+    attention launch records it (``_record_pv_execution``). ``out`` carries
+    the execution priority; the selected indices are its top ``M`` in
+    priority order. ``priority``: the cleaned score when the pooled softmax
+    already wrote it."""
     B, H, Q, K = score.shape
     P = (K + 1) // 2
     routing_state[STATE_KEY] = out["debt"].view(B, H, 1, P)
@@ -189,10 +188,10 @@ def _ledger_outputs(routing_state: dict, out: dict, score: torch.Tensor, layer_i
         }
     else:
         routing_state[_PV_SERVICE_PENDING] = (int(layer_idx), out["service"].view(B, H, 1, P))
-    if "priority" in out:
-        routing_state["cosa_value_risk_pair_priority"] = out["priority"]
+    routing_state["cosa_value_risk_pair_priority"] = out["priority"]
     routing_state["cosa_value_risk_pair_max_patch_blocks"] = int(M)
-    routing_state["cosa_value_risk_pair_selected_indices"] = out["index"][..., :M]
+    routing_state["cosa_value_risk_pair_selected_indices"] = ops.priority_order(out["priority"], M, out["index"],
+                                                                                out["count"], sink)
     # clamp_min(0) then NaN -> 0, as the reference's score (SW:3680-3684), in one pass
     if priority is None:
         sf = score.float()
@@ -492,9 +491,9 @@ def _select_for_layer(key: torch.Tensor, value: torch.Tensor, pooled_score: torc
         sel = ops.select_blocks(pooled_score, mode=_lib.MODE_VASC, topk=t or 0, innovation=innovation,
                                 row_cap=base, force_last=force_last, max_capacity=hint, sink_blocks=sink, debt=debt,
                                 pending_arrival=pending, prev_service=service,
-                                want_priority=not cfg.skip_routing_stats, want_mask=want_stats)
+                                want_priority=True, want_mask=want_stats)
         M = min(hint, orig_kblk)
-        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, M, cfg.service_domain, priority)
+        _ledger_outputs(routing_state, sel, pooled_score, layer_idx, M, cfg.service_domain, priority, sink)
         if want_stats:
             # the base map the reference hands its selector: Top-K (or the
             # cdf counts) plus the forced mixed tail (SW:7599-7662, 7750-7762)
