@@ -35,6 +35,7 @@
 // Top-K mode runs the select launch alone.
 #pragma clang fp contract(off)
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -294,16 +295,86 @@ __device__ __forceinline__ float settle_one(const SelectParams &p, int64_t i, fl
   return clamp_min0(u);
 }
 
+// Lane k's value of v (k uniform).
+__device__ __forceinline__ double read_lane(double v, int k) {
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b), k));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), k));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// Settlement of eight pairs per thread, j = j0 + kStride u (u < 8): settled
+// debt, reflection and consumed service. With all three ledger inputs present
+// the loads are unconditional (indices clamped into the head, results past P
+// unused), so all 24 are in flight together; otherwise settle_one per pair.
+constexpr int kSettleBatch = 8;
+template <int kStride>
+__device__ __forceinline__ void settle_batch(const SelectParams &p, int64_t bh, int64_t j0, float (&d)[kSettleBatch],
+                                             float (&refl)[kSettleBatch], float (&sig)[kSettleBatch]) {
+  if (p.debt_in && p.pending && p.prev_service) {
+    float a[kSettleBatch], b[kSettleBatch], c[kSettleBatch];
+#pragma unroll
+    for (int u = 0; u < kSettleBatch; ++u) {
+      const int64_t j = j0 + kStride * u < p.P ? j0 + kStride * u : p.P - 1;
+      a[u] = p.debt_in[bh * p.P + j];
+      b[u] = p.pending[bh * p.P + j];
+      c[u] = p.prev_service[bh * p.P + j];
+    }
+#pragma unroll
+    for (int u = 0; u < kSettleBatch; ++u) {
+      const float x = (clamp_min0(a[u]) + b[u]) - c[u];
+      sig[u] = c[u];
+      refl[u] = clamp_min0(-x);
+      d[u] = clamp_min0(x);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kSettleBatch; ++u) {
+      const int64_t j = j0 + kStride * u;
+      d[u] = refl[u] = sig[u] = 0.f;
+      if (j < p.P) d[u] = settle_one(p, bh * p.P + j, &refl[u], &sig[u]);
+    }
+  }
+}
+
+// Pair capacity of a head (sparse_wrapper.py:3788-3791): the mean of the
+// rows' pair-arrival sums, a wave sum over the rows (loads 16 rows per lane
+// at a time, their sum in order). One wave; every lane returns it.
+__device__ __forceinline__ float pair_capacity(const SelectParams &p, int64_t bh, int lane) {
+  double acc = 0.0;
+  for (int64_t q0 = lane; q0 < p.Q; q0 += 64 * 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = p.rowpair[bh * p.Q + (q0 + 64 * u < p.Q ? q0 + 64 * u : p.Q - 1)];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (q0 + 64 * u < p.Q) acc = acc + static_cast<double>(v[u]);
+  }
+  return static_cast<float>(wave_butterfly(acc) / static_cast<double>(p.Q));
+}
+
+// Admitted debt of one pair (sparse_wrapper.py:3852-3859 -> 1755-1769).
+__device__ __forceinline__ float admitted(float d, float dsum, float pc) {
+  const float scale = pc / floor_tiny(dsum);
+  return dsum > 0.f ? clamp01(d * scale) : 0.f;
+}
+
 // Global service gate (sparse_wrapper.py:3837-3842) from the per-head
-// partials; every caller recomputes the same bits.
-__device__ __forceinline__ int service_gate(const SelectParams &p) {
+// partials, summed in head order; every caller recomputes the same bits.
+// One wave: lane h loads head h's partials (64 heads at a time), and the
+// in-order float64 sums run over them lane by lane.
+__device__ __forceinline__ int service_gate(const SelectParams &p, int lane) {
   if (!p.pending) return 0;
   double u = 0.0, w = 0.0, c = 0.0;
-#pragma unroll 4
-  for (int64_t h = 0; h < p.BH; ++h) {  // sequential over heads; unrolled for loads in flight
-    u = u + p.gate_part[3 * h + 0];
-    w = w + p.gate_part[3 * h + 1];
-    c = c + p.gate_part[3 * h + 2];
+  for (int64_t h0 = 0; h0 < p.BH; h0 += 64) {
+    const int64_t h = h0 + lane < p.BH ? h0 + lane : p.BH - 1;
+    const double a = p.gate_part[3 * h + 0], b = p.gate_part[3 * h + 1], e = p.gate_part[3 * h + 2];
+    const int n = p.BH - h0 < 64 ? static_cast<int>(p.BH - h0) : 64;
+    for (int k = 0; k < n; ++k) {
+      u = u + read_lane(a, k);
+      w = w + read_lane(b, k);
+      c = c + read_lane(e, k);
+    }
   }
   const float fu = static_cast<float>(u), fw = static_cast<float>(w), fc = static_cast<float>(c);
   return (fc > 0.f) && (fu >= fw);
@@ -434,71 +505,91 @@ __global__ __launch_bounds__(1024) void arrival_kernel(const SelectParams p, int
 }
 
 // ------------------------------------------------------------------ head
-// Per head: ledger settlement, pending arrival (mean over rows), pair
-// capacity and admitted debt. Wave 0 of every workgroup recomputes the head's
-// debt sum and pair capacity (canonical wave sums); workgroup 0 of the head
-// also publishes the head's partials of the three global gate sums.
-// Waves 0-3 take 256 pairs each workgroup; wave 4 computes the head's sums
-// beside them (both are chains of dependent global loads, which now overlap).
-__global__ __launch_bounds__(320) void head_kernel(const SelectParams p) {
+// Per head, between the arrival and select passes: ledger settlement, pair
+// capacity, admitted debt and the select pass's (innovation, admitted debt)
+// table, the head's partials of the global gate; and the pending arrival
+// (the mean over rows of the pair arrival). Workgroup 0 of a head settles all
+// of its pairs (P <= 4096: eight per thread, every load in flight at once),
+// keeps the settled debt, reflection and consumed service in LDS for wave 0's
+// canonical wave sums, while wave 7 sums the pair capacity; the other
+// workgroups take 512 pairs each for the pending arrival (the chunk partials,
+// 64 loaded at a time, summed in chunk order).
+constexpr int kHeadThreads = 512;
+__global__ __launch_bounds__(kHeadThreads) void head_kernel(const SelectParams p) {
+  extern __shared__ float hl[];  // workgroup 0: settled debt, reflection, consumed service (3 P floats)
   __shared__ float sh_pc, sh_dsum;
   const int64_t bh = blockIdx.y;
-  const int tid = threadIdx.x;
-  // this thread's pair: its chunk partials and ledger inputs do not depend on
-  // the per-head sums below, so they load before the barrier
-  const int64_t pp = static_cast<int64_t>(blockIdx.x) * 256 + tid;
-  const bool has = tid < 256 && pp < p.P;
-  double acc_pp = 0.0;
-  float refl_pp = 0.f, sig_pp = 0.f, d_pp = 0.f;
-  if (has) {
-    const double *part = p.part + bh * p.nchunks * p.P + pp;
-    // 32 loads in flight per batch (C3 has 33 chunks); the sum keeps its order
-#pragma unroll 32
-    for (int64_t c = 0; c < p.nchunks; ++c) acc_pp = acc_pp + part[c * p.P];
-    d_pp = settle_one(p, bh * p.P + pp, &refl_pp, &sig_pp);
-  }
-  if (tid >= 256) {
-    const int lane = tid - 256;
-    double acc = 0.0, dacc = 0.0, useful = 0.0, wasted = 0.0, consumed = 0.0;
-    // unrolled so several iterations' loads are in flight; the float64 chains
-    // keep their order
-#pragma unroll 16
-    for (int64_t q = lane; q < p.Q; q += 64) acc = acc + static_cast<double>(p.rowpair[bh * p.Q + q]);
-#pragma unroll 8
-    for (int64_t j = lane; j < p.P; j += 64) {
-      float refl, sig;
-      const float d = settle_one(p, bh * p.P + j, &refl, &sig);
-      dacc = dacc + static_cast<double>(d);
-      useful = useful + static_cast<double>(clamp_min0(sig - refl));
-      wasted = wasted + static_cast<double>(refl);
-      consumed = consumed + static_cast<double>(sig);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t P = p.P;
+  if (blockIdx.x > 0) {
+    const int64_t pp = static_cast<int64_t>(blockIdx.x - 1) * kHeadThreads + tid;
+    if (pp >= P) return;
+    const double *part = p.part + bh * p.nchunks * P + pp;
+    double acc = 0.0;
+    for (int64_t c0 = 0; c0 < p.nchunks; c0 += 64) {
+      double v[64];
+#pragma unroll
+      for (int u = 0; u < 64; ++u) v[u] = part[(c0 + u < p.nchunks ? c0 + u : p.nchunks - 1) * P];
+#pragma unroll
+      for (int u = 0; u < 64; ++u)
+        if (c0 + u < p.nchunks) acc = acc + v[u];
     }
-    const double s = wave_butterfly(acc);
+    p.arrival_out[bh * P + pp] = static_cast<float>(acc / static_cast<double>(p.Q));
+    return;
+  }
+  float pc = 0.f;
+  if (w == 7) pc = pair_capacity(p, bh, lane);
+  float d[kSettleBatch], refl[kSettleBatch], sig[kSettleBatch], inn[kSettleBatch];
+#pragma unroll
+  for (int u = 0; u < kSettleBatch; ++u) {
+    const int64_t j = tid + kHeadThreads * u < P ? tid + kHeadThreads * u : P - 1;
+    inn[u] = p.innovation[bh * P + j];
+  }
+  settle_batch<kHeadThreads>(p, bh, tid, d, refl, sig);
+#pragma unroll
+  for (int u = 0; u < kSettleBatch; ++u) {
+    const int64_t j = tid + kHeadThreads * u;
+    if (j < P) {
+      hl[j] = d[u];
+      hl[P + j] = refl[u];
+      hl[2 * P + j] = sig[u];
+      p.debt_out[bh * P + j] = d[u];
+      p.counts[bh * P + j] = 0;
+    }
+  }
+  if (w == 7 && lane == 0) sh_pc = pc;
+  __syncthreads();
+  if (w == 0) {
+    double dacc = 0.0, useful = 0.0, wasted = 0.0, consumed = 0.0;
+    for (int64_t j = lane; j < P; j += 64) {
+      const float dj = hl[j], rj = hl[P + j], sj = hl[2 * P + j];
+      dacc = dacc + static_cast<double>(dj);
+      useful = useful + static_cast<double>(clamp_min0(sj - rj));
+      wasted = wasted + static_cast<double>(rj);
+      consumed = consumed + static_cast<double>(sj);
+    }
     const double ds = wave_butterfly(dacc);
     useful = wave_butterfly(useful);
     wasted = wave_butterfly(wasted);
     consumed = wave_butterfly(consumed);
     if (lane == 0) {
-      sh_pc = static_cast<float>(s / static_cast<double>(p.Q));
       sh_dsum = static_cast<float>(ds);
-      if (blockIdx.x == 0) {
-        p.gate_part[3 * bh + 0] = useful;
-        p.gate_part[3 * bh + 1] = wasted;
-        p.gate_part[3 * bh + 2] = consumed;
-      }
+      p.gate_part[3 * bh + 0] = useful;
+      p.gate_part[3 * bh + 1] = wasted;
+      p.gate_part[3 * bh + 2] = consumed;
     }
   }
   __syncthreads();
-  if (!has) return;
-  p.arrival_out[bh * p.P + pp] = static_cast<float>(acc_pp / static_cast<double>(p.Q));
-  p.counts[bh * p.P + pp] = 0;
-  const float d = d_pp;
-  p.debt_out[bh * p.P + pp] = d;
-  const float dsum = sh_dsum;
-  const float scale = sh_pc / floor_tiny(dsum);
-  const float admit = dsum > 0.f ? clamp01(d * scale) : 0.f;
-  p.adm[bh * p.P + pp] = admit;
-  p.ia[bh * p.P + pp] = float2{p.innovation[bh * p.P + pp], admit};
+  const float dsum = sh_dsum, pcap = sh_pc;
+#pragma unroll
+  for (int u = 0; u < kSettleBatch; ++u) {
+    const int64_t j = tid + kHeadThreads * u;
+    if (j < P) {
+      const float admit = admitted(d[u], dsum, pcap);
+      p.adm[bh * P + j] = admit;
+      p.ia[bh * P + j] = float2{inn[u], admit};
+    }
+  }
 }
 
 // ------------------------------------------------------------------ select
@@ -876,7 +967,7 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
   if (kVasc) {
     for (int64_t i = tid; i < (p.P + 1) / 2; i += 256) pair_cnt[i] = 0;  // packed pair counts
     __syncthreads();
-    gate = service_gate(p);
+    gate = service_gate(p, lane0);
   }
   const float2 *ia = kVasc ? p.ia + bh * p.P : nullptr;
   const uint32_t top = order_key(kFltMax);
@@ -1141,13 +1232,17 @@ __global__ __launch_bounds__(256) void select_kernel(const SelectParams p, int r
 
 // ------------------------------------------------------------------ service
 __global__ __launch_bounds__(256) void service_kernel(const SelectParams p) {
+  // the gate flag: wave 0 of workgroup 0 (the gate's sums take a whole wave)
+  if (p.gate_out && blockIdx.x == 0 && threadIdx.x < 64) {
+    const int g = service_gate(p, static_cast<int>(threadIdx.x));
+    if (threadIdx.x == 0) *p.gate_out = g;
+  }
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= p.BH * p.P) return;
   const int64_t pp = i % p.P;
   const float pair_size = (p.K % 2 && pp == p.P - 1) ? 1.0f : 2.0f;
   const float denom = pair_size * static_cast<float>(p.Q);
   p.service_out[i] = static_cast<float>(p.counts[i]) / denom;
-  if (i == 0 && p.gate_out) *p.gate_out = service_gate(p);
 }
 
 // ============================================================ register rows
@@ -1233,7 +1328,7 @@ void arrival_rows_kernel(const SelectParams p) {
   float x[EPT];
   for (int r0 = 0; r0 < nrows; r0 += kRowWaves) {
     if (r0 + w < nrows) {
-      const int64_t row = bh * p.Q + q0 + r0 + w;
+    const int64_t row = bh * p.Q + q0 + r0 + w;
       const float *srow = p.score + row * p.K;
       load_slots(x, srow, K, lane);
       int cap;
@@ -1337,34 +1432,36 @@ void arrival_rows_kernel(const SelectParams p) {
   }
 }
 
-// Candidate keys staged per lane by the select pass (kSeg or more: the row is
-// ranked on its registers instead). Lane l's r-th candidate sits at
-// cand[64 (r & 15) + l].
+// Candidate keys staged by the select pass: one list per wave, filled slot
+// by slot in lane order; up to kListCap of them (more: the row is ranked on
+// its registers instead), with room for one more slot's 64 past the cap.
 constexpr int kSeg = 16;
+constexpr int kListCap = 64 * kSeg - 64;
 // per wave: histogram (256 bins + 64 per-lane trash bins), 64 gathered keys
-// (+ 64 trash slots), candidate segments (64 kSeg words)
+// (+ 64 trash slots), the candidate list (64 kSeg words)
 constexpr int kRowWaveWords = 320 + 128 + 64 * kSeg;
 
 // The threshold of the keys of a padded row (64 EPT keys, 0 the smallest
 // any element can have, held by the padding): keys > T are kept, keys == T
 // in index order up to need (eqT of them). A histogram of a sample (every
-// lane's even slots; 256 bins over the sampled keys' range above 0)
+// lane's slots 0, 4, 8, ...; 256 bins over the sampled keys' range above 0)
 // brackets the c-th largest key at its sample rank c S / n -+ 3 sigma + 1
-// (half the keys sampled: about 2 n 3 sqrt(f (1 - f) / S) candidates, which
-// at 4096 keys and f = c / n = 1/4 stays well under kSeg per lane);
-// keys above the bracket are kept, the bracket's keys are staged per lane
-// and ranked exactly (rank_segs). When fewer than c keys exceed 0 the
-// threshold is 0, its ties going in index order. When the bracket misses,
-// or a lane holds kSeg or more candidates, the threshold is found by
-// bisection over the key bits.
+// (a quarter of the keys sampled: about 2 n 3 sqrt(f (1 - f) / S)
+// candidates, about 330 at 4096 keys and f = c / n = 1/4, well under
+// kListCap); keys above the bracket are kept, the bracket's keys go to the
+// wave's candidate list and are ranked exactly (rank_segs). When fewer than
+// c keys exceed 0 the threshold is 0, its ties going in index order. When
+// the bracket misses, or holds more than kListCap keys, the threshold is
+// found by bisection over the key bits.
+constexpr int kSampleStep = 4;  // sampled slots: m = 0, 4, 8, ...
 template <int EPT>
 __device__ __forceinline__ void rows_threshold(const uint32_t (&key)[EPT], int lane, int c, uint32_t *hist,
                                                uint32_t *sbuf, uint32_t *cand, uint32_t &T, int &need, int &eqT) {
   constexpr int n = 64 * EPT;
-  constexpr int S = 64 * ((EPT + 1) / 2);  // samples
+  constexpr int S = 64 * ((EPT + kSampleStep - 1) / kSampleStep);  // samples
   uint32_t smin = 0xffffffffu, smax = 0u;  // smin: over sampled keys above 0, less one
 #pragma unroll
-  for (int m = 0; m < EPT; m += 2) {
+  for (int m = 0; m < EPT; m += kSampleStep) {
     smin = min(smin, key[m] - 1u);
     smax = max(smax, key[m]);
   }
@@ -1384,7 +1481,7 @@ __device__ __forceinline__ void rows_threshold(const uint32_t (&key)[EPT], int l
     *reinterpret_cast<u32x4 *>(hist + 4 * lane) = u32x4{0, 0, 0, 0};
     wave_sync();
 #pragma unroll
-    for (int m = 0; m < EPT; m += 2) atomicAdd(&hist[key[m] ? (key[m] - smin) >> sh : 256u + lane], 1u);
+    for (int m = 0; m < EPT; m += kSampleStep) atomicAdd(&hist[key[m] ? (key[m] - smin) >> sh : 256u + lane], 1u);
     wave_sync();
     u32x4 h;
     const int suf = hist_suffix(hist, lane, h);
@@ -1396,31 +1493,31 @@ __device__ __forceinline__ void rows_threshold(const uint32_t (&key)[EPT], int l
     if (rs + mg <= spos) lo = smin + (static_cast<uint32_t>(rank_bin(h, suf, lane, rs + mg)) << sh);
     if (lo > hm1) lo = 1u;
   }
-  // candidates [lo, hm1] into this lane's segment (each key is written at
-  // the segment's end, which advances only past a candidate); keys above hm1 counted
+  // candidates [lo, hm1] appended to the wave's list slot by slot (each
+  // lane at its rank among the slot's candidate lanes; nothing is written
+  // once kListCap is passed); keys above hm1 counted
   const uint32_t span = hm1 - lo;
-  uint32_t *seg = cand + lane;
-  int cnt = 0, above = 0;
+  int above = 0, tot = 0;  // wave-uniform
+  uint32_t *trash = sbuf + 64 + lane;
 #pragma unroll
   for (int m = 0; m < EPT; ++m) {
     const uint32_t x = key[m];
     above += __popcll(__builtin_amdgcn_ballot_w64(x > hm1));
-    seg[64 * (cnt & (kSeg - 1))] = x;
-    cnt += x - lo <= span ? 1 : 0;  // keys below lo (0 among them) wrap above span
+    const bool in = x - lo <= span;  // keys below lo (0 among them) wrap above span
+    const uint64_t b = __builtin_amdgcn_ballot_w64(in);
+    // branch-free: every lane writes, the non-candidates to their trash slot;
+    // past kListCap the slot's candidates overwrite the list's last 64 entries
+    const uint32_t pos = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b), 0u));
+    uint32_t *at = (cand + (tot < kListCap ? tot : kListCap)) + pos;
+    *(in ? at : trash) = x;
+    tot += __popcll(b);
   }
-  above = __builtin_amdgcn_readfirstlane(above);
-  int tot = cnt, maxcnt = cnt;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    tot += __shfl_xor(tot, o);
-    maxcnt = max(maxcnt, __shfl_xor(maxcnt, o));
-  }
-  tot = __builtin_amdgcn_readfirstlane(tot);
-  maxcnt = __builtin_amdgcn_readfirstlane(maxcnt);
   wave_sync();
-  // a lane with kSeg candidates has overwritten its first one with the next key
-  if (above < c && above + tot >= c && maxcnt < kSeg) {
-    rank_segs(seg, cnt, maxcnt, lane, lo, hm1, c - above, hist, sbuf, T, need, eqT, 64);
+  if (above < c && above + tot >= c && tot <= kListCap) {
+    // lane l ranks list entries l, l + 64, ...
+    const int cnt = lane < tot ? (tot - lane + 63) / 64 : 0;
+    rank_segs(cand + lane, cnt, (tot + 63) / 64, lane, lo, hm1, c - above, hist, sbuf, T, need, eqT, 64);
     return;
   }
   if (above + tot < c && lo == 1u) {  // every key above 0 is kept; the rest of the c are 0 keys
@@ -1429,7 +1526,7 @@ __device__ __forceinline__ void rows_threshold(const uint32_t (&key)[EPT], int l
     eqT = n - above - tot;
     return;
   }
-  // the bracket missed, or a lane's candidates overflowed: the c-th largest
+  // the bracket missed, or held more than kListCap keys: the c-th largest
   // key by bisection over its bits (the largest t with at least c keys >= t),
   // exact for any distribution and holding no more registers than the keys
   uint32_t pre = 0u;
@@ -1458,11 +1555,11 @@ __device__ __forceinline__ void rows_threshold(const uint32_t (&key)[EPT], int l
 // score, otherwise its order key (the padding's key is 0 either way). VASC:
 // the (innovation, admitted debt) table of the head and the pair counts live
 // in LDS. Index lists are written in ascending order straight from the
-// ballots: every lane stores, the unselected ones past the row's buffer
-// range, which drops them.
+// ballots: the selected lanes of a slot store at their rank among them past
+// the slot's base (in the store's scalar offset) and count their pair.
 template <bool kVasc, int EPT, bool kPrefetch>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EPT <= 33 ? 4 : 1)))
-void select_rows_kernel(const SelectParams p, int rows_per_wave) {
+void select_rows_kernel(const SelectParams p, int rows_per_wave, int row_step) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int tid = threadIdx.x, lane0 = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1473,25 +1570,43 @@ void select_rows_kernel(const SelectParams p, int rows_per_wave) {
   uint32_t *pair_cnt = lds + kWaves * kRowWaveWords;  // 32 EPT words, one per pair (VASC)
   float2 *ia_s = reinterpret_cast<float2 *>(pair_cnt + 32 * EPT);  // 32 EPT entries (VASC), 0 past P
   const int64_t bh = blockIdx.y;
+  // this wave's rows: q_first + rr row_step, rr < rows_per_wave (consecutive
+  // rows when row_step is 1, else every row_step-th row of the head)
+  const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * kWaves + w;
+  const int64_t q_first = row_step == 1 ? wave_id * rows_per_wave : wave_id;
+  // the first row's scores load while the head's tables are set up (rows of
+  // up to 33 elements per lane: wider rows would lose a wave per SIMD to the
+  // registers held across the set-up)
+  constexpr bool kEarly = kPrefetch || EPT <= 33;
+  float x[EPT], nxt[EPT];
+  if (kEarly && q_first < p.Q) load_slots(kPrefetch ? nxt : x, p.score + (bh * p.Q + q_first) * p.K, K, lane0);
   int gate = 0;
   bool ia_fast = true;
   if (kVasc) {
+    // the head's table entries of this thread (indices clamped into the
+    // head; entries past P are zero), loaded before the gate's sums so that
+    // all the loads are in flight together
+    constexpr int kT = (32 * EPT + 255) / 256;
+    float2 t_ia[kT];
+#pragma unroll
+    for (int t = 0; t < kT; ++t) t_ia[t] = p.ia[bh * P + (tid + 256 * t < P ? tid + 256 * t : P - 1)];
+    gate = service_gate(p, lane0);
     bool bad = false;
-    for (int i = tid; i < 32 * EPT; i += 256) {
-      const float2 v = i < P ? p.ia[bh * P + i] : float2{0.f, 0.f};
-      ia_s[i] = v;
-      bad |= !(v.y <= kFltMax);
-      pair_cnt[i] = 0u;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      const int i = tid + 256 * t;
+      if (i < 32 * EPT) {
+        const float2 v = i < P ? t_ia[t] : float2{0.f, 0.f};
+        ia_s[i] = v;
+        bad |= !(v.y <= kFltMax);
+        pair_cnt[i] = 0u;
+      }
     }
     ia_fast = !__syncthreads_or(bad);
-    gate = service_gate(p);
   }
 
-  float x[EPT], nxt[EPT];
-  const int64_t q_first = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * rows_per_wave;
-  if (kPrefetch && q_first < p.Q) load_slots(nxt, p.score + (bh * p.Q + q_first) * p.K, K, lane0);
   for (int rr = 0; rr < rows_per_wave; ++rr) {
-    const int64_t q = q_first + rr;
+    const int64_t q = q_first + static_cast<int64_t>(rr) * row_step;
     if (q >= p.Q) break;
     // lane-derived values and masks are recomputed per row, not held across rows
     const int lane = opaque_lane(lane0);
@@ -1500,8 +1615,8 @@ void select_rows_kernel(const SelectParams p, int rows_per_wave) {
     if (kPrefetch) {
 #pragma unroll
       for (int m = 0; m < EPT; ++m) x[m] = nxt[m];
-      if (rr + 1 < rows_per_wave && q + 1 < p.Q) load_slots(nxt, srow + p.K, K, lane);
-    } else {
+      if (rr + 1 < rows_per_wave && q + row_step < p.Q) load_slots(nxt, srow + row_step * p.K, K, lane);
+    } else if (rr > 0 || !kEarly) {
       load_slots(x, srow, K, lane);
     }
     // ---- keys
@@ -1593,16 +1708,17 @@ void select_rows_kernel(const SelectParams p, int rows_per_wave) {
     const __amdgpu_buffer_rsrc_t irs =
         __builtin_amdgcn_make_buffer_rsrc(p.index_out + row * p.width, 0, static_cast<int>(4 * p.width), 0x00020000);
     uint32_t *cnt_l = pair_cnt + (lane >> 1);
-    int base = 0;
-    // one element slot: its ballot, the store (unselected lanes store past
-    // the buffer range, which drops them) and the pair count; the lane's
-    // position is computed by every lane (no exec-masked block per slot)
+    int base = 0;  // wave-uniform
+    // one element slot: its ballot; the selected lanes store their index at
+    // base + their rank among the slot's selected lanes (base in the store's
+    // scalar offset) and count their pair
     auto emit = [&](int m, bool sel) {
       const uint64_t bm = __builtin_amdgcn_ballot_w64(sel);
-      int pos = lanes_below(bm);
-      asm volatile("" : "+v"(pos));
-      __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(lane + 64 * m), irs,
-                                            sel ? 4 * (base + pos) : 0x7ffffff0u, 0, 0);
+      const uint32_t pos = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bm >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bm), 0u));
+      // branch-free: the unselected lanes store past the buffer range, which drops them
+      __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(lane + 64 * m), irs, sel ? 4 * pos : 0x7ffffff0u,
+                                            4 * base, 0);
       if (kVasc) atomicAdd(&cnt_l[32 * m], sel ? 1u : 0u);
       base += __popcll(bm);
     };
@@ -1952,18 +2068,41 @@ int launch_select_mode(const SelectParams &p, hipStream_t s) {
 
 // Register-row select for K <= 4096 (not with protected blocks or a forced
 // last block, which the staged kernel handles).
+// Workgroups of a register-row select kernel resident on the device at once
+// (queried once per kernel instantiation).
+template <bool kVasc, int EPT, typename Kern>
+int resident_workgroups(Kern kern, size_t lds_bytes) {
+  static std::atomic<int> cached{0};
+  int r = cached.load(std::memory_order_relaxed);
+  if (r) return r;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds_bytes) != hipSuccess)
+    cus = per_cu = 0;
+  r = cus * per_cu > 0 ? cus * per_cu : 1024;
+  cached.store(r, std::memory_order_relaxed);
+  return r;
+}
+
+// The rows of a head are dealt to its waves round-robin over a grid of at
+// most one resident round of workgroups (its share of the device per head),
+// so no partial second round of whole waves follows the first: a wave's
+// rows differ in number by at most one.
 template <bool kVasc, int EPT>
 int launch_select_rows_cfg(const SelectParams &p, hipStream_t s) {
-  const int64_t rows = p.BH * p.Q;
-  const int rpw = static_cast<int>(rows >= 4 * 8192 ? 4 : (rows >= 2 * 8192 ? 2 : 1));
   constexpr bool kPrefetch = false;
   // per wave rank buffers; VASC: pair counts (32 EPT words) and the (innovation, debt) table (32 EPT float2)
   const size_t lds_bytes = static_cast<size_t>(kWaves) * kRowWaveWords * 4 + (kVasc ? 384 * static_cast<size_t>(EPT) : 0);
-  const void *kern = reinterpret_cast<const void *>(select_rows_kernel<kVasc, EPT, kPrefetch>);
+  auto kern = select_rows_kernel<kVasc, EPT, kPrefetch>;
   int rc;
-  if ((rc = reserve_lds(kern, lds_bytes))) return rc;
-  const dim3 grid(static_cast<unsigned>(cdiv(p.Q, static_cast<int64_t>(kWaves) * rpw)), static_cast<unsigned>(p.BH));
-  hipLaunchKernelGGL((select_rows_kernel<kVasc, EPT, kPrefetch>), grid, dim3(256), lds_bytes, s, p, rpw);
+  if ((rc = reserve_lds(reinterpret_cast<const void *>(kern), lds_bytes))) return rc;
+  const int64_t per_head = cdiv(static_cast<int64_t>(resident_workgroups<kVasc, EPT>(kern, lds_bytes)), p.BH);
+  const int64_t need = cdiv(p.Q, static_cast<int64_t>(kWaves));
+  const int64_t gx = per_head < need ? per_head : need;
+  const int step = static_cast<int>(gx * kWaves);
+  const int rpw = static_cast<int>(cdiv(p.Q, static_cast<int64_t>(step)));
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(p.BH));
+  hipLaunchKernelGGL(kern, grid, dim3(256), lds_bytes, s, p, rpw, step);
   return check_launch("vasc_select_blocks/select");
 }
 
@@ -2093,8 +2232,9 @@ int launch_rows(const SelectParams &p, bool vasc, hipStream_t s) {
                          dim3(64 * aw), lds_bytes, s, p, static_cast<int>(bufn));
     }
     if ((rc = check_launch("vasc_select_blocks/arrival"))) return rc;
-    hipLaunchKernelGGL(head_kernel, dim3(static_cast<unsigned>(cdiv(p.P, 256)), static_cast<unsigned>(p.BH)),
-                       dim3(320), 0, s, p);
+    // workgroup 0 of a head settles its ledger, the others take 512 pairs each of the pending arrival
+    hipLaunchKernelGGL(head_kernel, dim3(static_cast<unsigned>(1 + cdiv(p.P, kHeadThreads)), static_cast<unsigned>(p.BH)),
+                       dim3(kHeadThreads), static_cast<size_t>(3 * p.P) * sizeof(float), s, p);
     if ((rc = check_launch("vasc_select_blocks/head"))) return rc;
   }
   if ((rc = launch_select(p, vasc, s))) return rc;
