@@ -1328,7 +1328,7 @@ void arrival_rows_kernel(const SelectParams p) {
   float x[EPT];
   for (int r0 = 0; r0 < nrows; r0 += kRowWaves) {
     if (r0 + w < nrows) {
-    const int64_t row = bh * p.Q + q0 + r0 + w;
+      const int64_t row = bh * p.Q + q0 + r0 + w;
       const float *srow = p.score + row * p.K;
       load_slots(x, srow, K, lane);
       int cap;
