@@ -2114,7 +2114,7 @@ int launch_select_rows(const SelectParams &p, hipStream_t s) {
   if (K <= 768) return launch_select_rows_cfg<kVasc, 12>(p, s);
   if (K <= 1088) return launch_select_rows_cfg<kVasc, 17>(p, s);
   if (K <= 1536) return launch_select_rows_cfg<kVasc, 24>(p, s);
-  if (K <= 2112 || !kVasc) return launch_select_rows_cfg<kVasc, 33>(p, s);
+  if (K <= 2112) return launch_select_rows_cfg<kVasc, 33>(p, s);
   if (K <= 3072) return launch_select_rows_cfg<kVasc, 48>(p, s);
   return launch_select_rows_cfg<kVasc, 64>(p, s);
 }
@@ -2177,12 +2177,10 @@ int launch_order(const OrderArgs &a, hipStream_t s) {
   return launch_order_npl<128>(a, s);
 }
 
-// Register rows serve VASC up to 4096 key blocks (after the register-row
-// arrival) and Top-K up to 2112; wider Top-K rows, protected blocks and a
-// forced last block take the staged kernel (measured faster for Top-K at
-// 4096 key blocks, where the register rows are load-latency bound).
+// Register rows serve both modes up to 4096 key blocks; protected blocks, a
+// forced last block and wider rows take the staged kernel.
 int launch_select(const SelectParams &p, bool vasc, hipStream_t s) {
-  if (!p.protected_mask && !p.force_last && p.K <= (vasc ? 64 * 64 : 33 * 64))
+  if (!p.protected_mask && !p.force_last && p.K <= 64 * 64)
     return vasc ? launch_select_rows<true>(p, s) : launch_select_rows<false>(p, s);
   return vasc ? launch_select_mode<true>(p, s) : launch_select_mode<false>(p, s);
 }
