@@ -199,6 +199,23 @@ def test_vasc_c3_shape_two_layers():
     _run_chain(2072, 1036, 16, 2, topk=224, force_last=False, sink=10, peak=2.0, seed=3)
 
 
+def test_vasc_c5_shape_two_layers():
+    """Config 5's widest rows (2048 x 4096 blocks, a quarter kept) over 8 heads:
+    each select wave takes six rows dealt round-robin across the head."""
+    _run_chain(4096, 2048, 8, 2, topk=1024, force_last=False, sink=0, peak=2.0, seed=5)
+
+
+def test_select_more_heads_than_resident_workgroups():
+    """1100 heads of 13 rows: one select workgroup per head walks all of its
+    rows (the grid exceeds one resident round); VASC and Top-K lists bit-exact."""
+    from vasc_amd import ops
+    _run_chain(130, 13, 1100, 2, topk=32, force_last=False, sink=1, peak=2.0, seed=11)
+    rng = np.random.default_rng(12)
+    score = _scores(rng, (1, 1100, 13, 130), peak=2.0)
+    out = ops.select_blocks(torch.from_numpy(score).cuda(), mode=TOPK, topk=32, sink_blocks=2)
+    _assert_lists(out, OS.topk_block_mask(score, 0, topk=32), 2)
+
+
 @pytest.mark.parametrize("K", [1, 2, 7, 130, 257, 518, 1036, 2072, 2113, 4096, 5000, 8192])
 def test_priority_order_bit_exact(K):
     """The selected indices (priority.topk(M, sorted=True)): every M from 1 to
