@@ -282,6 +282,66 @@ def test_cdf_counts_bit_exact(K, Q, H, levels):
             assert np.array_equal(base.cpu().numpy(), n + (fl & ~last_in & (n < K))), (thr, min_count, fl)
 
 
+def _cdf_rows(rng, K, n):
+    """Rows of every kind a cdf count meets, cycled: near-uniform softmax
+    (the C5 shape), peaked softmax, few distinct values, all equal (one
+    value), signed scores with zeros (a running sum that falls), NaN and
+    infinities, and mostly-zero rows."""
+    rows = []
+    for r in range(n):
+        kind = r % 7
+        if kind == 0:
+            x = _scores(rng, (K,), peak=0.13)
+        elif kind == 1:
+            x = _scores(rng, (K,), peak=3.0)
+        elif kind == 2:
+            x = _scores(rng, (K,), peak=1.0, levels=1)
+        elif kind == 3:
+            x = np.full(K, 1.0 / K, np.float32)
+        elif kind == 4:
+            x = (rng.standard_normal(K) * 0.01).astype(np.float32)
+            x[rng.random(K) < 0.2] = 0.0
+        elif kind == 5:
+            x = _scores(rng, (K,), peak=0.5)
+            x[rng.integers(0, K, 3)] = [np.nan, np.inf, -np.inf]
+        else:
+            x = np.zeros(K, np.float32)
+            x[rng.integers(0, K, 40)] = rng.random(40).astype(np.float32) / 40
+        rows.append(x)
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("K", [1025, 2048, 3000, 4096])
+def test_cdf_counts_row_kinds_bit_exact(K):
+    """cdf counts of rows of 1025..4096 blocks vs the oracle on every row
+    kind, ragged K, scalar and per-head thresholds, the ratio lower bound and
+    the forced tail."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(K + 7)
+    H, Q = 2, 15
+    score = _cdf_rows(rng, K, H * Q).reshape(1, H, Q, K)
+    s = torch.from_numpy(score).cuda()
+    for thr in (0.5, 0.9, 0.0, [0.3, 0.999]):
+        for min_count, fl in ((0, False), (K // 8, True)):
+            n = OS.cdf_counts(score, thr, min_count)
+            cnt, base = ops.cdf_counts(s, thr, min_count=min_count, force_last=fl, want_base=True)
+            assert np.array_equal(cnt.cpu().numpy(), n), (thr, min_count)
+            last_in = OS.select_top(score, n)[..., K - 1]
+            assert np.array_equal(base.cpu().numpy(), n + (fl & ~last_in & (n < K))), (thr, min_count, fl)
+
+
+def test_cdf_counts_c5_rows_bit_exact():
+    """C5's 4096-block rows (pooled softmax of near-uniform logits), 64 rows
+    at the two benchmark thresholds."""
+    from vasc_amd import ops
+    rng = np.random.default_rng(4096)
+    score = _scores(rng, (1, 4, 16, 4096), peak=0.13)
+    s = torch.from_numpy(score).cuda()
+    for thr in (0.5, 0.9):
+        cnt, _ = ops.cdf_counts(s, thr)
+        assert np.array_equal(cnt.cpu().numpy(), OS.cdf_counts(score, thr)), thr
+
+
 def test_cdf_counts_on_prefix_boundaries():
     """Dyadic scores: thresholds on, just under and within eps of exact prefix sums."""
     from vasc_amd import ops
