@@ -1303,7 +1303,10 @@ void arrival_rows_kernel(const SelectParams p) {
   constexpr int kStride = 32 * EPT;  // LDS row of pair arrivals
   constexpr int kPairs = (kStride + kThreads - 1) / kThreads;  // column partials per thread
   const int P = static_cast<int>(p.P), K = static_cast<int>(p.K);
-  const int64_t chunk = blockIdx.x, bh = blockIdx.y;
+  // chunks run from the last down, every head's chunk c together: the select
+  // pass sweeps each head's rows upward, so each pass starts on the rows the
+  // other read last, which the Infinity Cache may still hold
+  const int64_t lin = blockIdx.x, bh = lin % p.BH, chunk = p.nchunks - 1 - lin / p.BH;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t q0 = chunk * kChunk;
@@ -2198,7 +2201,7 @@ int launch_arrival_rows_cfg(const SelectParams &p, hipStream_t s) {
   int rc;
   if ((rc = reserve_lds(kern, lds_bytes))) return rc;
   hipLaunchKernelGGL((arrival_rows_kernel<EPT, kRowWaves>),
-                     dim3(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.BH)), dim3(64 * kRowWaves), lds_bytes,
+                     dim3(static_cast<unsigned>(p.nchunks * p.BH)), dim3(64 * kRowWaves), lds_bytes,
                      s, p);
   return VASC_OK;
 }
