@@ -235,6 +235,41 @@ def test_cdf_counts_sequential_float32_brute_force():
             assert got[0, h, q] == max(n, 1)
 
 
+def test_cdf_counts_brute_force_on_every_row_kind():
+    """Rows that are not softmax rows, against a loop written from the
+    definition alone: NaN first, then the values in descending order (-0 and
+    +0 equal), a strictly sequential float32 running sum, the count of the
+    prefix that stays <= T, then the fill rule. Row kinds: signed scores
+    with zeros (the sum falls), NaN and infinities, few distinct values, all
+    equal, mostly zero."""
+    rng = np.random.default_rng(13)
+    K = 300
+    rows = [
+        (rng.standard_normal(K) * 0.01).astype(np.float32),
+        _softmax(rng.standard_normal(K) * 0.5),
+        _softmax(np.round(rng.standard_normal(K))),
+        np.full(K, 1.0 / K, np.float32),
+        np.zeros(K, np.float32),
+    ]
+    rows[0][rng.random(K) < 0.2] = 0.0
+    rows[0][:3] = [-0.0, 0.0, -0.0]
+    rows[1][rng.integers(0, K, 3)] = [np.nan, np.inf, -np.inf]
+    rows[4][rng.integers(0, K, 20)] = rng.random(20).astype(np.float32) / 20
+    s = np.stack(rows).reshape(1, 1, len(rows), K)
+    for thr in (0.0, 0.02, 0.5, 0.9, 1.0):
+        got = OS.cdf_counts(s, thr)
+        T = np.float32(np.float32(thr) + np.float32(1e-5))
+        for q, row in enumerate(rows):
+            order = sorted(range(K), key=lambda i: (not np.isnan(row[i]), -float(row[i]) if not np.isnan(row[i]) else 0.0, i))
+            acc, n = np.float32(0.0), 0
+            for i in order:
+                acc = np.float32(acc + row[i])
+                if not acc <= T:
+                    break
+                n += 1
+            assert got[0, 0, q] == max(n, 1), (thr, q)
+
+
 def test_cdf_counts_closed_forms():
     K = 256
     u = np.full((1, 1, 2, K), 1.0 / K, np.float32)  # cdf[i] = (i+1)/K exactly
