@@ -250,11 +250,15 @@ def test_cdf_counts_brute_force_on_every_row_kind():
         _softmax(np.round(rng.standard_normal(K))),
         np.full(K, 1.0 / K, np.float32),
         np.zeros(K, np.float32),
+        _softmax(rng.standard_normal(K) * 0.5),
+        _softmax(rng.standard_normal(K) * 0.5),
     ]
     rows[0][rng.random(K) < 0.2] = 0.0
     rows[0][:3] = [-0.0, 0.0, -0.0]
-    rows[1][rng.integers(0, K, 3)] = [np.nan, np.inf, -np.inf]
+    rows[1][rng.integers(0, K, 2)] = np.nan          # NaN sorts first: the count is 1
     rows[4][rng.integers(0, K, 20)] = rng.random(20).astype(np.float32) / 20
+    rows[5][[7, 11]] = [np.inf, -np.inf]
+    rows[6][13] = -np.inf                             # last: counted once the sum reaches it
     s = np.stack(rows).reshape(1, 1, len(rows), K)
     for thr in (0.0, 0.02, 0.5, 0.9, 1.0):
         got = OS.cdf_counts(s, thr)
